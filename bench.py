@@ -1,0 +1,255 @@
+#!/usr/bin/env python3
+"""MoE layer fwd+bwd throughput on one MI355X (HIP kernels through the op API).
+
+One step = routing (top-k softmax) -> permute -> fc1 grouped GEMM -> SwiGLU x
+probs -> fc2 grouped GEMM -> unpermute, forward and backward, on one batch of
+synthetic inputs already resident in HBM (``MoELayer.forward_with_logits``
+with every op served by the HIP providers). Default workload: the
+Qwen3-30B-A3B-shaped layer (16384 tokens, hidden 2048, 128 experts, top-8,
+ffn 768, bf16, Zipf-skewed fp32 router logits).
+
+Prints one JSON line with the throughput, the grouped-GEMM roofline (HIP
+events around every grouped-GEMM launch on the compute stream) and the CPU
+oracle timed on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0
+GEMM_ENTRIES = ("tt_gmm_fwd", "tt_gmm_dgrad", "tt_gmm_wgrad", "tt_gmm_fp8_fwd", "tt_gmm_fp8_dgrad")
+PERMUTE_ENTRIES = ("tt_permute_scatter", "tt_unpermute_gather")
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default="qwen3_30b_a3b")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-budget-s", type=float, default=20.0)
+    return p.parse_args()
+
+
+def build_layer(w, device):
+    import torch.nn.functional as F
+
+    from torchturbo_amd import configs as C
+    from torchturbo_amd.moe import Fp8GroupedMLP, GroupedMLP, MoEConfig, MoELayer, MoESubmodules, ModuleSpec
+
+    cfg = MoEConfig(
+        hidden_size=w.hidden, num_moe_experts=w.experts, moe_ffn_hidden_size=w.ffn,
+        gated_linear_unit=True, activation_func=F.silu, moe_router_topk=w.topk,
+        moe_router_pre_softmax=w.pre_softmax, moe_router_score_function=w.score_function,
+        moe_router_num_groups=w.num_groups, moe_router_group_topk=w.group_topk,
+        moe_router_topk_scaling_factor=w.scaling_factor, params_dtype=w.dtype,
+        moe_router_enable_expert_bias=w.expert_bias, perform_initialization=False,
+    )
+    experts = Fp8GroupedMLP if w.fp8 else GroupedMLP
+    layer = MoELayer(cfg, None, submodules=MoESubmodules(experts=ModuleSpec(module=experts)))
+    layer = layer.to(device)
+    w1, w2 = C.make_weights(w, device=device)
+    with torch.no_grad():
+        if w.fp8:
+            q1, s1 = C.fp8_blocks(w1.transpose(1, 2).contiguous())
+            q2, s2 = C.fp8_blocks(w2.transpose(1, 2).contiguous())
+            layer.experts.load_quantized(q1, s1, q2, s2)
+        else:
+            layer.experts.weight1.copy_(w1.reshape(-1, 2 * w.ffn))
+            layer.experts.weight2.copy_(w2.reshape(-1, w.hidden))
+        bias = C.make_expert_bias(w, device=device)
+        if bias is not None:
+            layer.router.expert_bias.copy_(bias)
+    del w1, w2
+    shared = None
+    if w.shared_ffn:
+        g = torch.Generator(device=device).manual_seed(w.seed + 9)
+        mk = lambda *s: torch.empty(*s, device=device).normal_(0, 0.02, generator=g).to(w.dtype)  # noqa: E731
+        gate, up, down = (mk(w.shared_ffn, w.hidden), mk(w.shared_ffn, w.hidden),
+                          mk(w.hidden, w.shared_ffn))
+        for t in (gate, up, down):
+            t.requires_grad_()
+
+        def shared(x):
+            return F.linear(F.silu(F.linear(x, gate)) * F.linear(x, up), down)
+    return layer, shared
+
+
+def gpu_run(w, steps, warmup):
+    from torchturbo_amd import _lib as L
+    from torchturbo_amd import configs as C
+    from torchturbo_amd.dispatch import OpPolicy, get_or_create_ops
+    from torchturbo_amd.runtime import CudaRuntime
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    get_or_create_ops(device_runtime=CudaRuntime(), default_policy=OpPolicy.CUSTOM)
+    layer, shared = build_layer(w, dev)
+    hidden = C.make_hidden(w, device=dev).requires_grad_()
+    logits = C.make_logits(w, device=dev).requires_grad_()
+    grad = C.make_grad(w, device=dev)
+    params = [p for p in layer.parameters() if p.requires_grad]
+
+    def step():
+        for p in params:
+            p.grad = None
+        hidden.grad = None
+        logits.grad = None
+        out = layer.forward_with_logits(hidden, logits)
+        if shared is not None:
+            out = out + shared(hidden)
+        out.backward(grad)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = L.KernelTimer(GEMM_ENTRIES + PERMUTE_ENTRIES)
+    L.set_timer(timer)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.set_timer(None)
+    kernels = timer.elapsed_ms()
+    return (t1 - t0) * 1e3 / steps, kernels
+
+
+def cpu_baseline(w, budget_s):
+    """The CPU oracle (the reference's native composition) on a token sample."""
+    from dataclasses import replace
+
+    from oracle import layer as o_layer
+    from oracle.fp8 import dequantize_experts
+    from torchturbo_amd import configs as C
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    full = C.resolve(w)
+    w1, w2 = C.make_weights(full)
+    if full.fp8:
+        q1, s1 = C.fp8_blocks(w1.transpose(1, 2).contiguous())
+        q2, s2 = C.fp8_blocks(w2.transpose(1, 2).contiguous())
+        fp8 = {"q1": q1, "s1": s1, "q2": q2, "s2": s2,
+               "m1": dequantize_experts(q1, s1).requires_grad_(),
+               "m2": dequantize_experts(q2, s2).requires_grad_()}
+        w1 = w2 = None
+    else:
+        fp8 = None
+        w1.requires_grad_()
+        w2.requires_grad_()
+    cfg = o_layer.RoutingConfig(topk=w.topk, pre_softmax=w.pre_softmax,
+                                score_function=w.score_function, num_groups=w.num_groups,
+                                group_topk=w.group_topk, scaling_factor=w.scaling_factor)
+    bias = C.make_expert_bias(full)
+    tokens = 128
+    result = None
+    while True:
+        sw = replace(full, tokens=tokens, logits="zipf" if full.logits == "varlen" else full.logits)
+        hidden = C.make_hidden(sw).requires_grad_()
+        logits = C.make_logits(sw).requires_grad_()
+        grad = C.make_grad(sw)
+        t0 = time.perf_counter()
+        out = o_layer.moe_layer(hidden, logits, w1, w2, cfg, expert_bias=bias, fp8=fp8)
+        out.backward(grad)
+        dt = time.perf_counter() - t0
+        result = (tokens, dt)
+        if dt * 2.2 > budget_s or tokens * 2 > full.tokens:
+            break
+        tokens *= 2
+    tokens, dt = result
+    return {
+        "value": round(tokens / dt, 2),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{tokens} of {full.tokens} tokens of the {full.name} layer "
+                   f"(all {full.experts} experts, full weights), one fwd+bwd, "
+                   f"{dt:.2f} s, torch {torch.__version__} CPU, {cores} threads"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU (EP=1); --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    from torchturbo_amd import configs as C
+
+    w = C.resolve(C.WORKLOADS[args.workload])
+    ms, kernels = gpu_run(w, args.steps, args.warmup)
+    tokens_per_s = w.tokens / (ms / 1e3)
+
+    gemm_launches = sum(kernels.get(n, (0, 0.0))[0] for n in GEMM_ENTRIES)
+    gemm_ms = sum(kernels.get(n, (0, 0.0))[1] for n in GEMM_ENTRIES)
+    flops_step = w.gemm_flops_fwd_bwd()
+    per_launch_flops = flops_step * args.steps / max(gemm_launches, 1)
+    avg_launch_s = gemm_ms / 1e3 / max(gemm_launches, 1)
+    achieved_tflops = per_launch_flops / avg_launch_s / 1e12 if avg_launch_s > 0 else 0.0
+
+    perm_n, perm_ms = kernels.get("tt_permute_scatter", (0, 0.0))
+    unperm_n, unperm_ms = kernels.get("tt_unpermute_gather", (0, 0.0))
+    pass_bytes = w.permute_bytes()
+    perm_gbs = pass_bytes / (perm_ms / 1e3 / perm_n) / 1e9 if perm_n else None
+    unperm_gbs = pass_bytes / (unperm_ms / 1e3 / unperm_n) / 1e9 if unperm_n else None
+
+    line = {
+        "metric": "MoE layer fwd+bwd tokens/sec on 1 MI355X; grouped-GEMM % MFMA peak",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 weights, bf16" if w.fp8 else str(w.dtype).replace("torch.", "").replace("bfloat16", "bf16"),
+        "data": "synthetic",
+        "config": {
+            "workload": w.name, "tokens": w.tokens, "hidden": w.hidden, "experts": w.experts,
+            "topk": w.topk, "ffn": w.ffn, "router": w.score_function,
+            "routed_rows": w.routed_rows, "gemm_tflop_per_step": round(flops_step / 1e12, 4),
+            "parallelism": "ep1",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "grouped GEMM (tt_gmm_*; fc1/fc2 fwd, dgrad, wgrad)",
+            "achieved": round(achieved_tflops, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "launches": gemm_launches,
+            "avg_launch_us": round(avg_launch_s * 1e6, 1),
+            "gemm_ms_per_step": round(gemm_ms / args.steps, 3),
+        },
+        "permute": {
+            "bound": "hbm", "unit": "GB/s", "peak": HBM_PEAK_GBS,
+            "permute_scatter_gbs": None if perm_gbs is None else round(perm_gbs, 1),
+            "unpermute_gather_gbs": None if unperm_gbs is None else round(unperm_gbs, 1),
+            "bytes_per_pass": pass_bytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_budget_s)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

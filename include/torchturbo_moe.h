@@ -1,0 +1,184 @@
+/*
+ * C-ABI of the MI355X (gfx950) MoE expert-path kernels.
+ *
+ * Every entry point takes raw device pointers, element counts, dtype enums
+ * and a hipStream_t (passed as void*), enqueues its kernels on that stream and
+ * returns a status: TT_OK, or a negative code with a message available from
+ * tt_last_error(). Entry points never allocate device memory: buffers (and
+ * workspaces, sized by the *_workspace helpers) come from the caller, and no
+ * entry point synchronises the host. Integer results (routing ids, row maps,
+ * counts) are deterministic; floating-point reductions use a fixed order.
+ *
+ * Each declaration names the reference interface it replaces (paths relative
+ * to the TorchTurbo checkout: src/torchturbo/...).
+ */
+#ifndef TORCHTURBO_MOE_H
+#define TORCHTURBO_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtypes */
+enum { TT_F32 = 0, TT_BF16 = 1, TT_F16 = 2, TT_F8E4M3 = 3 };
+/* status codes */
+enum { TT_OK = 0, TT_ERR_INVALID = -1, TT_ERR_UNSUPPORTED = -2, TT_ERR_HIP = -3 };
+/* router score functions */
+enum { TT_SCORE_SOFTMAX = 0, TT_SCORE_SIGMOID = 1, TT_SCORE_SQRTSOFTPLUS = 2 };
+
+/* ABI version of this header; bumped on any signature change. */
+int tt_abi_version(void);
+/* Message of the last failing call on this host thread ("" if none). */
+const char* tt_last_error(void);
+
+/* ---- Router -------------------------------------------------------------
+ * Replaces topk_softmax_with_capacity / group_limited_topk
+ * (models/modules/moe/utils.py:30-80,127-230), called from
+ * TopKRouter.routing (models/modules/moe/router.py:277-356).
+ * logits [T, E] (f32/bf16/f16) -> probs [T, E] (logits dtype, zeros except
+ * the k selected), routing_map [T, E] (bytes 0/1), top_indices [T, k] int64
+ * in descending-score order (ties: lower expert id first).
+ * expert_bias [E] f32 or NULL (selection only). num_groups/group_topk = 0
+ * disable group-limited selection. scaling_factor = 0 means none.
+ * fixed_indices [T, k] int64 or NULL: hash routing (ids given).
+ * Supports E <= 1024, k <= 64, k <= E. */
+int tt_router_topk_fwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                       int32_t num_experts, int32_t topk, int32_t score_function,
+                       int32_t pre_softmax, const float* expert_bias, int32_t num_groups,
+                       int32_t group_topk, float scaling_factor, const int64_t* fixed_indices,
+                       void* probs, uint8_t* routing_map, int64_t* top_indices, void* stream);
+
+/* Backward of tt_router_topk_fwd: grad_probs [T, E] (logits dtype) ->
+ * grad_logits [T, E] (logits dtype). Autograd of utils.py:175-228. */
+int tt_router_topk_bwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                       int32_t num_experts, int32_t topk, int32_t score_function,
+                       int32_t pre_softmax, float scaling_factor, const int64_t* top_indices,
+                       const void* grad_probs, void* grad_logits, void* stream);
+
+/* ---- Routing index (counting sort by expert) ----------------------------
+ * Replaces the index build of TorchMoEMaskPermutation
+ * (ops/providers/native/moe_permutation.py:36-56: masked_select of token ids,
+ * masked_scatter_ of packed rows, gather by expert_indices) and the counts of
+ * MoEAlltoAllTokenDispatcher.preprocess (models/modules/moe/token_dispatcher.py:125-147).
+ * expert_indices [T, k] int64 (distinct per token) ->
+ *   row_indices [T, k] int32: packed row of (t, slot j), rows ordered by
+ *     expert then token (ops/moe.py:10-46);
+ *   token_of_row [T*k] int32: source token of each packed row;
+ *   packed_probs [T*k] (probs dtype) = probs_dense[t, e] of each row, if both
+ *     pointers are non-NULL;
+ *   tokens_per_expert [E] int64.
+ * Invalid ids (outside [0, E)) are not written anywhere; the call then
+ * reports nothing on the host (no synchronisation), so callers validate ids.
+ * Workspace: tt_route_index_workspace(T, E) bytes. */
+size_t tt_route_index_workspace(int64_t num_tokens, int32_t num_experts);
+int tt_route_index(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
+                   int32_t num_experts, const void* probs_dense, int probs_dtype,
+                   int32_t* row_indices, int32_t* token_of_row, void* packed_probs,
+                   int64_t* tokens_per_expert, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* ---- Permute / unpermute -------------------------------------------------
+ * Token rows -> packed rows: packed[row_indices[t, j]] = tokens[t].
+ * Replaces the index_select of native moe_permutation.py:43 (and TE
+ * moe_permute, ops/providers/cuda/moe_permutation.py:77-81); also the
+ * backward of unweighted unpermutation. dtype f32/bf16/f16. */
+int tt_permute_scatter(const void* tokens, int dtype, int64_t num_tokens, int64_t hidden,
+                       int32_t topk, const int32_t* row_indices, void* packed, void* stream);
+
+/* out[t] = sum_j packed[r_j] (* probs[t, expert_indices[t, j]]) over the
+ * token's rows r_j in ascending row order, accumulated in fp32 and rounded
+ * once to the packed dtype; the weight product is rounded to the promoted
+ * dtype first. Replaces TorchMoEMaskUnpermutation
+ * (ops/providers/native/moe_permutation.py:68-99) and, with probs == NULL,
+ * the index_select backward of the permutation. probs [T, E] or NULL. */
+int tt_unpermute_gather(const void* packed, int dtype, int64_t num_tokens, int64_t hidden,
+                        int32_t topk, const int32_t* row_indices, const int64_t* expert_indices,
+                        const void* probs, int probs_dtype, int32_t num_experts, void* out,
+                        void* stream);
+
+/* Backward of weighted tt_unpermute_gather: grad_packed[r_j] =
+ * (grad_out[t] * w_j) cast to the packed dtype; grad_probs [T, E] (probs
+ * dtype) = sum_h grad_out[t, h] * packed[r_j, h] at (t, expert_j), zero
+ * elsewhere. Autograd of moe_permutation.py:90-98. */
+int tt_unpermute_gather_bwd(const void* grad_out, const void* packed, int dtype,
+                            int64_t num_tokens, int64_t hidden, int32_t topk,
+                            const int32_t* row_indices, const int64_t* expert_indices,
+                            const void* probs, int probs_dtype, int32_t num_experts,
+                            void* grad_packed, void* grad_probs, void* stream);
+
+/* Backward of the packed-probs gather: grad_probs_dense [T, E] =
+ * grad_packed_probs[row_indices[t, j]] at (t, expert_indices[t, j]), zero
+ * elsewhere (autograd of the masked_select at moe_permutation.py:44-46). */
+int tt_packed_probs_bwd(const void* grad_packed_probs, int dtype, int64_t num_tokens,
+                        int32_t topk, int32_t num_experts, const int32_t* row_indices,
+                        const int64_t* expert_indices, void* grad_probs_dense, void* stream);
+
+/* Chunk reorder: output = concat(input chunk sorted_idxs[0], chunk
+ * sorted_idxs[1], ...) for row chunks of sizes split_sizes (device int64
+ * [C]); also applied to probs [rows] when both pointers are non-NULL.
+ * Replaces TorchMoESortChunks (ops/providers/native/moe_permutation.py:110-126)
+ * and TE moe_sort_chunks_by_index (ops/providers/cuda/moe_permutation.py:159-197).
+ * C <= 4096. */
+int tt_sort_chunks(const void* input, int dtype, int64_t rows, int64_t hidden,
+                   const int64_t* split_sizes, const int64_t* sorted_idxs, int32_t num_chunks,
+                   const void* probs, int probs_dtype, void* output, void* out_probs,
+                   void* stream);
+
+/* ---- SwiGLU and probability weighting ------------------------------------
+ * x [rows, 2F] = [gate | up] -> out [rows, F]:
+ * a = round(round(silu(gate)) * up); with probs [rows] (non-NULL)
+ * out = round(a * p) in the promoted dtype. Replaces native swiglu
+ * (ops/providers/native/swiglu.py:10-12) and GroupedMLP.activation_func_with_probs
+ * (models/modules/moe/experts.py:181-186). */
+int tt_swiglu_fwd(const void* x, int dtype, int64_t rows, int64_t ffn, const void* probs,
+                  int probs_dtype, void* out, void* stream);
+
+/* Backward: grad_out [rows, F] -> grad_x [rows, 2F] (x dtype) and, if
+ * grad_probs is non-NULL, grad_probs [rows] (probs dtype) = sum_f
+ * grad_out * a. */
+int tt_swiglu_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, const void* probs,
+                  int probs_dtype, const void* grad_out, void* grad_x, void* grad_probs,
+                  void* stream);
+
+/* ---- Grouped GEMM over expert segments ----------------------------------
+ * Rows of x are grouped by expert: expert e owns counts[e] consecutive rows
+ * (counts: device int64 [E]; sum(counts) == M). Replaces
+ * TorchGroupedMatmul (ops/providers/native/grouped_matmul.py:16-56) and
+ * grouped_gemm.ops.gmm (ops/providers/cuda/grouped_matmul.py:34-36).
+ * dtype bf16/f16 (MFMA, fp32 accumulation) or f32.
+ * fwd:   y[M, N] = x[M, K] @ W[e] with W [E, K, N]; trans_b: W [E, N, K], W[e]^T. */
+int tt_gmm_fwd(const void* x, const void* w, int dtype, int64_t m, int64_t k, int64_t n,
+               int32_t num_experts, int32_t trans_b, const int64_t* counts, void* y,
+               void* stream);
+/* dgrad: dx[M, K] = dy[M, N] @ W[e]^T (trans_b: dy @ W[e]). */
+int tt_gmm_dgrad(const void* dy, const void* w, int dtype, int64_t m, int64_t k, int64_t n,
+                 int32_t num_experts, int32_t trans_b, const int64_t* counts, void* dx,
+                 void* stream);
+/* wgrad: dW[e] = x_e^T @ dy_e ([E, K, N]); trans_b: dy_e^T @ x_e ([E, N, K]).
+ * Experts with no rows get zeros. */
+int tt_gmm_wgrad(const void* x, const void* dy, int dtype, int64_t m, int64_t k, int64_t n,
+                 int32_t num_experts, int32_t trans_b, const int64_t* counts, void* dw,
+                 void* stream);
+
+/* FP8 e4m3 weights with 128x128 block scales, HF [out, in] orientation:
+ * qw [E, N, K] bytes, scale [E, ceil(N/128), ceil(K/128)] (bf16 or f32).
+ * Weight element = bf16(f32(q) * f32(scale)), the rule of the reference's
+ * offline dequantizer (scripts/dequant/bailing.py:57-102,
+ * scripts/dequant/dequantize.py:62-78), applied while staging the operand.
+ * fwd: y[M, N] = x[M, K] @ deq(qw[e])^T; dgrad: dx[M, K] = dy[M, N] @ deq(qw[e]).
+ * x / dy / y / dx are bf16. */
+int tt_gmm_fp8_fwd(const void* x, const uint8_t* qw, const void* scale, int scale_dtype,
+                   int64_t m, int64_t k, int64_t n, int32_t num_experts,
+                   const int64_t* counts, void* y, void* stream);
+int tt_gmm_fp8_dgrad(const void* dy, const uint8_t* qw, const void* scale, int scale_dtype,
+                     int64_t m, int64_t k, int64_t n, int32_t num_experts,
+                     const int64_t* counts, void* dx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCHTURBO_MOE_H */

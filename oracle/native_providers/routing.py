@@ -1,0 +1,116 @@
+"""Native top-k routing (CPU oracle).
+
+Restates ``topk_softmax_with_capacity`` and ``group_limited_topk`` of
+``src/torchturbo/models/modules/moe/utils.py:30-80,127-230``:
+
+* ``softmax``, post-top-k (default; Qwen3 ``norm_topk_prob`` and Mixtral):
+  ``probs = softmax(topk(logits).values)`` in fp32 (``:190-196``);
+* ``softmax``, pre-top-k: ``softmax(logits)`` in fp32, top-k of it (or of it
+  plus the fp32 expert bias, then gathered) (``:181-189``);
+* ``sigmoid`` / ``sqrtsoftplus``: fp32 scores, optional bias for selection
+  only, renormalised with ``+1e-20`` when ``topk > 1`` (``:197-217``);
+* group-limited selection: group score = sum of the top ``topk // group_topk``
+  scores of each group; keep ``group_topk`` groups; top-k inside them (``:30-80``);
+* token-id hash routing takes the ids from ``hash_table[input_ids]``;
+* ``scaling_factor`` multiplies after normalisation (``:221-222``); probs are
+  cast to the logits dtype (``:224``) and scattered to a dense [T, E] tensor
+  and a boolean map (``:227-228``).
+
+Ties: PyTorch's CPU ``topk`` has no documented tie rule. The HIP router
+breaks ties toward the lower expert id; inputs used for bit-exact routing
+comparisons use fp32 logits, where ties have measure zero, and the tie rule
+itself is pinned by ``tests/test_router_ties.py`` on the CPU.
+
+Pinned by: the KATs of ``tests/models/test_moe_router.py:74-171`` and
+``tests/models/test_moe_adapter_routing.py:179-243`` restated in
+``tests/test_oracle_kats.py`` and a brute-force sort on tiny inputs.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from torchturbo_amd.dispatch import OpImpl, OpImplKind, register_op
+
+
+def group_limited_topk(scores, topk, num_tokens, num_experts, num_groups, group_topk):
+    per_group = num_experts // num_groups
+    group_scores = (
+        scores.view(num_tokens, num_groups, per_group)
+        .topk(topk // group_topk, dim=-1)[0].sum(dim=-1)
+    )
+    keep = torch.topk(group_scores, k=group_topk, dim=-1, sorted=False)[1]
+    group_mask = torch.zeros_like(group_scores).scatter_(1, keep, 1)
+    expert_mask = (
+        group_mask.unsqueeze(-1).expand(num_tokens, num_groups, per_group)
+        .reshape(num_tokens, num_experts)
+    )
+    masked = scores.masked_fill(~expert_mask.bool(), float("-inf"))
+    return torch.topk(masked, k=topk, dim=-1)
+
+
+def topk_softmax_with_capacity(
+    logits, topk, use_pre_softmax=False, num_groups=None, group_topk=None,
+    scaling_factor=None, score_function="softmax", expert_bias=None,
+    use_hash_routing=False, hash_table=None, input_ids=None,
+):
+    assert logits.dim() == 2, f"Expected 2D logits [num_tokens, num_experts], got {logits.dim()}."
+    num_tokens, num_experts = logits.shape
+
+    def select(scores):
+        if group_topk:
+            return group_limited_topk(scores, topk, num_tokens, num_experts,
+                                      num_groups, group_topk)
+        return torch.topk(scores, k=topk, dim=1)
+
+    if score_function == "softmax":
+        if use_hash_routing:
+            assert hash_table is not None and input_ids is not None
+            top_indices = hash_table[input_ids]
+        if use_pre_softmax:
+            scores = torch.softmax(logits, dim=-1, dtype=torch.float32)
+            if use_hash_routing:
+                probs = scores.gather(1, top_indices)
+            elif expert_bias is not None:
+                top_indices = select(scores + expert_bias.float())[1]
+                probs = scores.gather(1, top_indices)
+            else:
+                probs, top_indices = select(scores)
+        else:
+            if use_hash_routing:
+                top_scores = logits.gather(1, top_indices)
+            else:
+                top_scores, top_indices = select(logits)
+            probs = torch.softmax(top_scores, dim=-1, dtype=torch.float32)
+    elif score_function in ("sigmoid", "sqrtsoftplus"):
+        if score_function == "sigmoid":
+            scores = torch.sigmoid(logits.float())
+        else:
+            scores = F.softplus(logits.float()).sqrt()
+        if use_hash_routing:
+            assert hash_table is not None and input_ids is not None
+            top_indices = hash_table[input_ids]
+            scores = scores.gather(1, top_indices)
+        elif expert_bias is not None:
+            top_indices = select(scores + expert_bias.float())[1]
+            scores = scores.gather(1, top_indices)
+        else:
+            scores, top_indices = select(scores)
+        probs = scores / (scores.sum(dim=-1, keepdim=True) + 1e-20) if topk > 1 else scores
+    else:
+        raise ValueError(f"Invalid score_function: {score_function}")
+
+    if scaling_factor:
+        probs = probs * scaling_factor
+    probs = probs.type_as(logits)
+    dense = torch.zeros_like(logits).scatter(1, top_indices, probs)
+    routing_map = torch.zeros_like(logits).int().scatter(1, top_indices, 1).bool()
+    return dense, routing_map, top_indices
+
+
+@register_op(op_name="topk_softmax_with_capacity", impl_name="torch_topk_softmax",
+             kind=OpImplKind.NATIVE, priority=0, devices=())
+class TorchTopKSoftmax(OpImpl):
+    def __call__(self, logits, topk, **kwargs):
+        return topk_softmax_with_capacity(logits, topk, **kwargs)

@@ -1,0 +1,136 @@
+"""The MoE layer on the GPU (HIP providers) vs the CPU oracle layer, fwd + bwd.
+
+Tolerance (bf16): normwise max relative error <= 2e-2 and mean relative
+error <= 2e-3 on the output and on every gradient; routing ids and the
+per-expert counts are bit-exact (fp32 logits).
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import layer as o_layer
+from tests.conftest import assert_bf16_close, rel_errors
+from torchturbo_amd import configs as C
+from torchturbo_amd.dispatch import OpPolicy
+from torchturbo_amd.moe import Fp8GroupedMLP, GroupedMLP, MoEConfig, MoELayer, MoESubmodules, ModuleSpec
+from torchturbo_amd.runtime import CudaRuntime
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def build_layer(w: C.Workload, w1, w2, fp8=False):
+    cfg = MoEConfig(
+        hidden_size=w.hidden, num_moe_experts=w.experts, moe_ffn_hidden_size=w.ffn,
+        gated_linear_unit=True, activation_func=F.silu, moe_router_topk=w.topk,
+        moe_router_pre_softmax=w.pre_softmax, moe_router_score_function=w.score_function,
+        moe_router_num_groups=w.num_groups, moe_router_group_topk=w.group_topk,
+        moe_router_topk_scaling_factor=w.scaling_factor, params_dtype=w.dtype,
+        moe_router_enable_expert_bias=w.expert_bias,
+    )
+    experts = Fp8GroupedMLP if fp8 else GroupedMLP
+    layer = MoELayer(cfg, None, submodules=MoESubmodules(experts=ModuleSpec(module=experts)))
+    layer = layer.to(DEV)
+    if not fp8:
+        with torch.no_grad():
+            layer.experts.weight1.copy_(w1.reshape(-1, 2 * w.ffn))
+            layer.experts.weight2.copy_(w2.reshape(-1, w.hidden))
+    return layer
+
+
+def scaled(w: C.Workload, **kw) -> C.Workload:
+    return replace(w, **kw)
+
+
+LAYER_CASES = [
+    C.TOY,
+    scaled(C.QWEN3, tokens=512, hidden=256, ffn=128),
+    scaled(C.MIXTRAL, tokens=256, hidden=512, ffn=384),
+    scaled(C.QWEN3, name="varlen_small", tokens=0, hidden=256, ffn=128, logits="varlen"),
+]
+
+
+@pytest.mark.parametrize("w", LAYER_CASES, ids=lambda w: w.name)
+def test_layer_fwd_bwd_matches_oracle(process_ops, w):
+    process_ops(CudaRuntime(), OpPolicy.CUSTOM)
+    w = C.resolve(w)
+    if w.name == "varlen_small":
+        w = replace(w, tokens=2048)
+    hidden = C.make_hidden(w)
+    logits = C.make_logits(w)
+    w1, w2 = C.make_weights(w)
+    grad = C.make_grad(w)
+
+    # oracle (CPU)
+    hr = hidden.clone().requires_grad_()
+    lr = logits.clone().requires_grad_()
+    w1r = w1.clone().requires_grad_()
+    w2r = w2.clone().requires_grad_()
+    cfg = o_layer.RoutingConfig(topk=w.topk, pre_softmax=w.pre_softmax,
+                                score_function=w.score_function, num_groups=w.num_groups,
+                                group_topk=w.group_topk, scaling_factor=w.scaling_factor)
+    out_r, trace = o_layer.moe_layer(hr, lr, w1r, w2r, cfg, trace=True)
+    out_r.backward(grad)
+
+    # HIP path
+    layer = build_layer(w, w1, w2)
+    hd = hidden.to(DEV).requires_grad_()
+    ld = logits.to(DEV).requires_grad_()
+    out = layer.forward_with_logits(hd, ld)
+    out.backward(grad.to(DEV))
+    assert out.dtype == w.dtype
+    assert torch.equal(layer.token_dispatcher.tokens_per_expert.cpu(), trace.tokens_per_expert)
+    tol = dict(max_rel=1e-4, mean_rel=1e-5) if w.dtype == torch.float32 else {}
+    assert_bf16_close(out.cpu(), out_r, what="out", **tol)
+    assert_bf16_close(hd.grad.cpu(), hr.grad, what="d_hidden", **tol)
+    assert_bf16_close(ld.grad.cpu(), lr.grad, what="d_logits", **tol)
+    g1 = layer.experts.weight1.grad.view(w.experts, w.hidden, 2 * w.ffn).cpu()
+    g2 = layer.experts.weight2.grad.view(w.experts, w.ffn, w.hidden).cpu()
+    assert_bf16_close(g1, w1r.grad, what="d_w1", **tol)
+    assert_bf16_close(g2, w2r.grad, what="d_w2", **tol)
+
+
+def test_fp8_layer_matches_dequantized_oracle(process_ops):
+    process_ops(CudaRuntime(), OpPolicy.CUSTOM)
+    w = scaled(C.DSV3, tokens=256, hidden=512, ffn=256, experts=16, num_groups=4, group_topk=2,
+               shared_ffn=None)
+    hidden = C.make_hidden(w)
+    logits = C.make_logits(w)
+    bias = C.make_expert_bias(w)
+    m1, m2 = C.make_weights(w)  # [E, H, 2F], [E, F, H]
+    hf1 = m1.transpose(1, 2).contiguous()  # [E, 2F, H]  (out, in)
+    hf2 = m2.transpose(1, 2).contiguous()  # [E, H, F]
+    q1, s1 = C.fp8_blocks(hf1)
+    q2, s2 = C.fp8_blocks(hf2)
+    grad = C.make_grad(w)
+
+    from oracle.fp8 import dequantize_experts
+    d1 = dequantize_experts(q1, s1).requires_grad_()
+    d2 = dequantize_experts(q2, s2).requires_grad_()
+    hr = hidden.clone().requires_grad_()
+    lr = logits.clone().requires_grad_()
+    cfg = o_layer.RoutingConfig(topk=w.topk, score_function=w.score_function,
+                                num_groups=w.num_groups, group_topk=w.group_topk,
+                                scaling_factor=w.scaling_factor)
+    out_r = o_layer.moe_layer(hr, lr, None, None, cfg, expert_bias=bias,
+                              fp8={"q1": q1, "s1": s1, "q2": q2, "s2": s2, "m1": d1, "m2": d2})
+    out_r.backward(grad)
+
+    layer = build_layer(w, None, None, fp8=True)
+    layer.experts.load_quantized(q1.to(DEV), s1.to(DEV), q2.to(DEV), s2.to(DEV))
+    with torch.no_grad():
+        layer.router.expert_bias.copy_(bias.to(DEV))
+    hd = hidden.to(DEV).requires_grad_()
+    ld = logits.to(DEV).requires_grad_()
+    out = layer.forward_with_logits(hd, ld)
+    out.backward(grad.to(DEV))
+    assert_bf16_close(out.cpu(), out_r, what="out")
+    assert_bf16_close(hd.grad.cpu(), hr.grad, what="d_hidden")
+    assert_bf16_close(ld.grad.cpu(), lr.grad, what="d_logits")
+    assert_bf16_close(layer.experts.master1.grad.cpu(), d1.grad, what="d_w1")
+    assert_bf16_close(layer.experts.master2.grad.cpu(), d2.grad, what="d_w2")

@@ -1,0 +1,426 @@
+"""HIP kernels vs the CPU oracle, op by op (GPU).
+
+Integer results (routing ids, routing map, packed-row map, counts, packed
+rows) are compared bit-exactly. The fp32-accumulated gather-sums are
+compared bit-exactly too (same order, same rounding as the reference's CPU
+``scatter_add_`` / ``index_add_``). Floating-point math that goes through
+``exp`` or a GEMM is compared within the path's tolerance: normwise max
+relative error <= 2e-2 and mean relative error <= 2e-3 for bf16 (tighter
+for fp32 where stated).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.native_providers import grouped_matmul as o_gmm
+from oracle.native_providers import moe_permutation as o_perm
+from oracle.native_providers import routing as o_route
+from oracle.native_providers import swiglu as o_swiglu
+from oracle import fp8 as o_fp8
+from oracle import route_np
+from tests.conftest import assert_bf16_close, rel_errors
+from torchturbo_amd.dispatch import MoEPermutation
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def distinct_ids(T, E, k, seed, skew=False):
+    g = torch.Generator().manual_seed(seed)
+    scores = torch.rand(T, E, generator=g)
+    if skew:
+        scores += torch.linspace(2.0, 0.0, E)
+    return scores.topk(k, dim=1).indices
+
+
+# ---------------------------------------------------------------------------
+# Router
+# ---------------------------------------------------------------------------
+ROUTER_CASES = [
+    # (T, E, k, score, pre, groups, gtopk, scale, bias, dtype)
+    (257, 8, 2, "softmax", False, None, None, None, False, torch.float32),
+    (1000, 128, 8, "softmax", False, None, None, None, False, torch.float32),
+    (300, 128, 8, "softmax", True, None, None, 2.0, False, torch.float32),
+    (300, 128, 8, "softmax", True, None, None, None, True, torch.float32),
+    (200, 256, 8, "sigmoid", False, 8, 4, 2.5, True, torch.float32),
+    (200, 256, 8, "sigmoid", False, None, None, None, False, torch.float32),
+    (200, 64, 6, "sqrtsoftplus", False, None, None, 1.5, False, torch.float32),
+    (64, 512, 8, "softmax", True, 8, 4, 2.5, True, torch.float32),
+    (77, 16, 1, "softmax", False, None, None, None, False, torch.float32),
+    (77, 16, 1, "sigmoid", False, None, None, None, False, torch.float32),
+    (500, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", ROUTER_CASES, ids=lambda c: f"T{c[0]}E{c[1]}k{c[2]}{c[3]}{'pre' if c[4] else ''}g{c[5]}{str(c[9])[6:]}")
+def test_router_matches_oracle(hip_ops, case):
+    T, E, k, score, pre, groups, gtopk, scale, use_bias, dtype = case
+    g = torch.Generator().manual_seed(T * 31 + E)
+    logits = torch.randn(T, E, generator=g).to(dtype)
+    bias = (torch.randn(E, generator=g) * 0.05) if use_bias else None
+    kwargs = dict(use_pre_softmax=pre, num_groups=groups, group_topk=gtopk, scaling_factor=scale,
+                  score_function=score, expert_bias=bias)
+    ref_logits = logits.clone().requires_grad_()
+    probs_r, map_r, ids_r = o_route.topk_softmax_with_capacity(ref_logits, k, **kwargs)
+    dev_logits = logits.to(DEV).requires_grad_()
+    probs, rmap, ids = hip_ops.topk_softmax_with_capacity(
+        dev_logits, k, **{**kwargs, "expert_bias": None if bias is None else bias.to(DEV)})
+    if dtype == torch.float32:
+        # Bit-exact selection (no ties with fp32 N(0, 1) logits).
+        assert torch.equal(ids.cpu(), ids_r)
+        assert torch.equal(rmap.cpu(), map_r)
+    else:
+        # bf16 logits tie at the k-th score for some tokens; compare the
+        # selected *sets* where the k-th and (k+1)-th scores differ.
+        srt = logits.float().sort(dim=1, descending=True).values
+        clean = srt[:, k - 1] != srt[:, k] if k < E else torch.ones(T, dtype=torch.bool)
+        assert torch.equal(rmap.cpu()[clean], map_r[clean])
+    assert probs.dtype == dtype
+    tol = 2e-6 if dtype == torch.float32 else 8e-3
+    mx, _ = rel_errors(probs.cpu(), probs_r)
+    assert mx <= tol, mx
+    # backward through the dense probs
+    w = torch.randn(T, E, generator=g).to(dtype)
+    (probs_r * w).sum().backward()
+    (probs * w.to(DEV)).sum().backward()
+    if dtype == torch.float32:
+        mx, mean = rel_errors(dev_logits.grad.cpu(), ref_logits.grad)
+        assert mx <= 1e-5 and mean <= 1e-6, (mx, mean)
+    else:
+        clean_rows = clean
+        assert_bf16_close(dev_logits.grad.cpu()[clean_rows], ref_logits.grad[clean_rows], what="dlogits")
+
+
+def test_router_hash_routing(hip_ops):
+    T, E, k = 40, 32, 4
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(T, E, generator=g)
+    table = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(10)])
+    input_ids = torch.randint(0, 10, (T,), generator=g)
+    for score in ("softmax", "sigmoid"):
+        for pre in (False, True):
+            kw = dict(use_pre_softmax=pre, score_function=score, use_hash_routing=True,
+                      hash_table=table, input_ids=input_ids, scaling_factor=1.7)
+            pr, mr, ir = o_route.topk_softmax_with_capacity(logits, k, **kw)
+            p, m, i = hip_ops.topk_softmax_with_capacity(
+                logits.to(DEV), k, **{**kw, "hash_table": table.to(DEV), "input_ids": input_ids.to(DEV)})
+            assert torch.equal(i.cpu(), ir)
+            assert torch.equal(m.cpu(), mr)
+            assert rel_errors(p.cpu(), pr)[0] <= 2e-6
+
+
+def test_router_low_precision_selection(hip_ops):
+    # KAT: tests/models/test_moe_router.py:74-83
+    for score in ("softmax", "sigmoid", "sqrtsoftplus"):
+        for dtype in (torch.bfloat16, torch.float16):
+            logits = torch.tensor([[0.0, 0.0001]], dtype=dtype, device=DEV)
+            _, rmap, ids = hip_ops.topk_softmax_with_capacity(logits, 1, use_pre_softmax=True,
+                                                               score_function=score)
+            assert rmap.cpu().tolist() == [[False, True]]
+            assert ids.cpu().tolist() == [[1]]
+
+
+def test_router_ties_go_to_lower_expert(hip_ops):
+    logits = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0]], device=DEV)
+    _, _, ids = hip_ops.topk_softmax_with_capacity(logits, 2)
+    assert ids.cpu().tolist() == [[1, 2]]
+
+
+# ---------------------------------------------------------------------------
+# Routing index + permutation
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("T,E,k,skew", [(1, 4, 1, False), (255, 8, 2, False), (256, 8, 2, True),
+                                        (1000, 128, 8, True), (3000, 256, 8, False),
+                                        (513, 64, 16, True), (100, 1000, 3, False)])
+def test_route_index_bit_exact(T, E, k, skew):
+    from torchturbo_amd.providers.hip._functions import route_index
+
+    ids = distinct_ids(T, E, k, seed=T + E, skew=skew)
+    probs = torch.rand(T, E)
+    rows, tor, pprobs, counts = route_index(ids.to(DEV), E, probs.to(DEV))
+    r_rows, r_tor, r_counts, _ = route_np.route_index(ids.numpy(), E)
+    assert np.array_equal(rows.cpu().numpy(), r_rows)
+    assert np.array_equal(tor.cpu().numpy(), r_tor)
+    assert np.array_equal(counts.cpu().numpy(), r_counts)
+    order = np.argsort(ids.reshape(-1).numpy(), kind="stable")
+    flat_ids = ids.reshape(-1).numpy()[order]
+    expected_probs = probs.numpy()[order // k, flat_ids]
+    assert np.array_equal(pprobs.cpu().numpy(), expected_probs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,H,E,k", [(300, 256, 8, 2), (517, 136, 64, 6), (64, 2048, 128, 8)])
+def test_permutation_and_unpermutation_bit_exact(hip_ops, dtype, T, H, E, k):
+    g = torch.Generator().manual_seed(T + H)
+    ids = distinct_ids(T, E, k, seed=T)
+    rmap = torch.zeros(T, E, dtype=torch.bool).scatter(1, ids, True)
+    x = torch.randn(T, H, generator=g).to(dtype)
+    probs = torch.rand(T, E, generator=g) * rmap
+    ref = o_perm.permute(x, rmap, probs=probs, expert_indices=ids)
+    got = hip_ops.moe_permutation(x.to(DEV), rmap.to(DEV), probs=probs.to(DEV),
+                                  expert_indices=ids.to(DEV))
+    assert torch.equal(got.row_indices.cpu(), ref.row_indices)
+    assert torch.equal(got.tokens.cpu(), ref.tokens)
+    assert torch.equal(got.probs.cpu(), ref.probs)
+    assert torch.equal(got.tokens_per_expert.cpu(), rmap.sum(0))
+    # unpermutation of arbitrary expert outputs: unweighted and weighted
+    y = torch.randn(T * k, H, generator=g).to(dtype)
+    for w in (None, probs, probs.to(torch.bfloat16)):
+        perm_r = MoEPermutation(y, None, ref.row_indices, ids)
+        perm_g = MoEPermutation(y.to(DEV), None, got.row_indices, ids.to(DEV))
+        out_r = o_perm.unpermute(perm_r, torch.Size([T, H]), probs=w)
+        out_g = hip_ops.moe_unpermutation(perm_g, torch.Size([T, H]),
+                                          probs=None if w is None else w.to(DEV))
+        assert out_g.dtype == out_r.dtype
+        assert torch.equal(out_g.cpu(), out_r), f"weights={None if w is None else w.dtype}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_permutation_backward(hip_ops, dtype):
+    T, H, E, k = 200, 128, 16, 4
+    g = torch.Generator().manual_seed(3)
+    ids = distinct_ids(T, E, k, seed=9)
+    rmap = torch.zeros(T, E, dtype=torch.bool).scatter(1, ids, True)
+    x = torch.randn(T, H, generator=g).to(dtype)
+    probs = torch.rand(T, E, generator=g) * rmap
+    gy = torch.randn(T * k, H, generator=g).to(dtype)
+    gp = torch.randn(T * k, generator=g)
+    xr, pr = x.clone().requires_grad_(), probs.clone().requires_grad_()
+    ref = o_perm.permute(xr, rmap, probs=pr, expert_indices=ids)
+    torch.autograd.backward([ref.tokens, ref.probs], [gy, gp])
+    xd, pd = x.to(DEV).requires_grad_(), probs.to(DEV).requires_grad_()
+    got = hip_ops.moe_permutation(xd, rmap.to(DEV), probs=pd, expert_indices=ids.to(DEV))
+    torch.autograd.backward([got.tokens, got.probs], [gy.to(DEV), gp.to(DEV)])
+    assert torch.equal(xd.grad.cpu(), xr.grad)  # fp32 gather-sum in row order
+    assert torch.equal(pd.grad.cpu(), pr.grad)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_unpermutation_backward(hip_ops, dtype):
+    T, H, E, k = 150, 192, 12, 3
+    g = torch.Generator().manual_seed(4)
+    ids = distinct_ids(T, E, k, seed=2)
+    rmap = torch.zeros(T, E, dtype=torch.bool).scatter(1, ids, True)
+    rows = o_perm.permute(torch.zeros(T, 1), rmap, expert_indices=ids).row_indices
+    y = torch.randn(T * k, H, generator=g).to(dtype)
+    probs = torch.rand(T, E, generator=g)
+    go = torch.randn(T, H, generator=g).to(dtype)
+    for weighted in (False, True):
+        yr = y.clone().requires_grad_()
+        pr = probs.clone().requires_grad_() if weighted else None
+        out_r = o_perm.unpermute(MoEPermutation(yr, None, rows, ids), torch.Size([T, H]), probs=pr)
+        out_r.backward(go)
+        yd = y.to(DEV).requires_grad_()
+        pd = probs.to(DEV).requires_grad_() if weighted else None
+        out_d = hip_ops.moe_unpermutation(MoEPermutation(yd, None, rows.to(DEV), ids.to(DEV)),
+                                          torch.Size([T, H]), probs=pd)
+        out_d.backward(go.to(DEV))
+        assert torch.equal(yd.grad.cpu(), yr.grad)
+        if weighted:
+            mx, mean = rel_errors(pd.grad.cpu(), pr.grad)
+            assert mx <= 1e-5 and mean <= 1e-6, (mx, mean)
+
+
+def test_permutation_kats(hip_ops):
+    # tests/ops/test_moe_permutation_contract.py:72-84
+    r = hip_ops.moe_permutation(torch.tensor([[2.0], [3.0]], device=DEV),
+                                torch.tensor([[False, True], [True, False]], device=DEV),
+                                probs=torch.tensor([[0.0, 0.5], [0.25, 0.0]], device=DEV))
+    assert r.tokens.cpu().tolist() == [[3.0], [2.0]]
+    assert r.probs.cpu().tolist() == [0.25, 0.5]
+    assert r.row_indices.cpu().tolist() == [[1], [0]]
+    # :307-370 (mixed providers case, custom both sides)
+    tokens = torch.tensor([[10.0], [20.0], [30.0]], device=DEV, requires_grad=True)
+    probs = torch.tensor([[0.25, 0.0, 0.5], [0.0, 0.75, 0.125], [0.125, 0.25, 0.0]],
+                         device=DEV, requires_grad=True)
+    mask = probs.detach().bool()
+    idx = torch.tensor([[0, 2], [1, 2], [0, 1]], device=DEV)
+    m = hip_ops.moe_permutation(tokens, mask, probs=probs, expert_indices=idx)
+    assert m.tokens.detach().cpu().flatten().tolist() == [10.0, 30.0, 20.0, 30.0, 10.0, 20.0]
+    assert m.row_indices.cpu().tolist() == [[0, 4], [2, 5], [1, 3]]
+    out = hip_ops.moe_unpermutation(m, tokens.shape, probs=probs)
+    assert out.detach().cpu().flatten().tolist() == [7.5, 17.5, 11.25]
+    out.sum().backward()
+    assert tokens.grad.cpu().flatten().tolist() == probs.detach().sum(1).cpu().tolist()
+    torch.testing.assert_close(probs.grad.cpu(), (tokens.detach().expand_as(probs) * mask).cpu())
+    un = hip_ops.moe_unpermutation(m, tokens.shape)
+    assert un.detach().cpu().flatten().tolist() == [20.0, 40.0, 60.0]
+    # :412-434 probability precision is retained
+    packed = torch.tensor([[1.0], [-1.0]], dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    p = torch.tensor([[1.00390625, 1.0]], device=DEV, requires_grad=True)
+    mp = MoEPermutation(packed, None, torch.tensor([[0, 1]], dtype=torch.int32, device=DEV),
+                        torch.tensor([[0, 1]], device=DEV))
+    o = hip_ops.moe_unpermutation(mp, torch.Size([1, 1]), probs=p)
+    assert o.dtype == torch.bfloat16 and o.item() == 0.00390625
+    o.sum().backward()
+    assert p.grad.cpu().tolist() == [[1.0, -1.0]]
+    # :37-69 small contributions survive (fp32 accumulation), bf16 and fp16
+    for dtype, large in ((torch.bfloat16, 256), (torch.float16, 2048)):
+        packed = torch.tensor([[large], [-large], [1], [2], [-large], [large]], dtype=dtype, device=DEV)
+        mp = MoEPermutation(packed, None, torch.tensor([[0, 2, 4], [5, 1, 3]], dtype=torch.int32, device=DEV),
+                            torch.tensor([[0, 1, 2], [2, 0, 1]], device=DEV))
+        o = hip_ops.moe_unpermutation(mp, torch.Size([2, 1]))
+        assert o.cpu().float().flatten().tolist() == [1.0, 2.0]
+
+
+def test_permutation_empty_and_zero_weight(hip_ops):
+    tokens = torch.empty(0, 4, device=DEV, requires_grad=True)
+    probs = torch.empty(0, 3, device=DEV, requires_grad=True)
+    m = hip_ops.moe_permutation(tokens, probs.detach().bool(), probs=probs,
+                                expert_indices=torch.empty(0, 2, dtype=torch.long, device=DEV))
+    out = hip_ops.moe_unpermutation(m, tokens.shape, probs)
+    out.sum().backward()
+    assert out.shape == (0, 4)
+    # zero-probability selections keep their rows and router gradient
+    t = torch.tensor([[2.0]], device=DEV)
+    p = torch.tensor([[0.0, 1.0]], device=DEV, requires_grad=True)
+    r = hip_ops.moe_permutation(t, torch.tensor([[True, True]], device=DEV), probs=p,
+                                expert_indices=torch.tensor([[0, 1]], device=DEV))
+    assert r.tokens.cpu().tolist() == [[2.0], [2.0]]
+    (r.tokens * r.probs[:, None]).sum().backward()
+    assert p.grad.cpu().tolist() == [[2.0, 2.0]]
+
+
+def test_permute_unpermute_round_trip_full_qwen_size(hip_ops):
+    """Size-independent property at the Qwen3 shape: unpermute(permute(x)) == k * x."""
+    from torchturbo_amd.configs import QWEN3, make_logits
+
+    T, H, E, k = QWEN3.tokens, QWEN3.hidden, QWEN3.experts, QWEN3.topk
+    logits = make_logits(QWEN3)
+    _, rmap_r, ids_r = o_route.topk_softmax_with_capacity(logits, k)
+    probs, rmap, ids = hip_ops.topk_softmax_with_capacity(logits.to(DEV), k)
+    assert torch.equal(ids.cpu(), ids_r)
+    x = torch.randn(T, H, device=DEV).to(torch.bfloat16)
+    m = hip_ops.moe_permutation(x, rmap, probs=probs, expert_indices=ids)
+    r_rows, _, r_counts, _ = route_np.route_index(ids_r.numpy(), E)
+    assert np.array_equal(m.row_indices.cpu().numpy(), r_rows)
+    assert np.array_equal(m.tokens_per_expert.cpu().numpy(), r_counts)
+    back = hip_ops.moe_unpermutation(m, x.shape)
+    assert torch.equal(back, (x.float() * k).to(torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU (+ probs)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("with_probs", [False, True])
+def test_swiglu_matches_oracle(hip_ops, dtype, with_probs):
+    rows, F = 333, 96
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(rows, 2 * F, generator=g) * 2).to(dtype)
+    p = torch.rand(rows, generator=g)
+    go = torch.randn(rows, F, generator=g).to(dtype)
+    xr = x.clone().requires_grad_()
+    pr = p.clone().requires_grad_()
+    ref = o_swiglu.swiglu_probs(xr, pr) if with_probs else o_swiglu.swiglu(xr)
+    ref.backward(go)
+    xd = x.to(DEV).requires_grad_()
+    pd = p.to(DEV).requires_grad_()
+    got = hip_ops.swiglu_probs(xd, pd) if with_probs else hip_ops.swiglu(xd)
+    got.backward(go.to(DEV))
+    assert got.dtype == ref.dtype
+    if dtype == torch.float32:
+        assert rel_errors(got.cpu(), ref)[0] <= 1e-6
+        assert rel_errors(xd.grad.cpu(), xr.grad)[0] <= 1e-5
+    else:
+        # at most one ulp away where exp() differs in the last fp32 bit
+        assert_bf16_close(got.cpu(), ref, max_rel=8e-3, mean_rel=1e-4, what="swiglu")
+        assert_bf16_close(xd.grad.cpu(), xr.grad, max_rel=1e-2, mean_rel=1e-3, what="dx")
+    if with_probs:
+        mx, mean = rel_errors(pd.grad.cpu(), pr.grad)
+        assert mx <= 1e-3 and mean <= 1e-4, (mx, mean)
+
+
+# ---------------------------------------------------------------------------
+# Grouped GEMM
+# ---------------------------------------------------------------------------
+def _ref_gmm(x, w, counts, trans_b):
+    return o_gmm.grouped_matmul(x.double(), w.double(), counts, trans_b=trans_b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("counts,K,N", [([0, 5, 0, 11], 64, 32), ([300, 0, 17, 513, 1], 256, 384),
+                                        ([1024] * 4, 512, 768), ([0, 0, 0], 128, 128)])
+def test_grouped_matmul_fwd_bwd(hip_ops, dtype, trans_b, counts, K, N):
+    g = torch.Generator().manual_seed(sum(counts) + K)
+    E = len(counts)
+    M = sum(counts)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(E, N, K, generator=g) if trans_b else torch.randn(E, K, N, generator=g)).mul(0.05).to(dtype)
+    dy = torch.randn(M, N, generator=g).to(dtype)
+    xr = x.double().requires_grad_()
+    wr = w.double().requires_grad_()
+    yr = o_gmm.grouped_matmul(xr, wr, counts, trans_b=trans_b)
+    yr.backward(dy.double())
+    xd = x.to(DEV).requires_grad_()
+    wd = w.to(DEV).requires_grad_()
+    for cnt in (counts, torch.tensor(counts), torch.tensor(counts, device=DEV)):
+        xd.grad = None
+        wd.grad = None
+        y = hip_ops.grouped_matmul(xd, wd, cnt, trans_b=trans_b)
+        y.backward(dy.to(DEV))
+        assert y.shape == (M, N) and y.dtype == dtype
+        if M == 0:
+            assert torch.count_nonzero(wd.grad) == 0
+            continue
+        tol = (1e-5, 1e-6) if dtype == torch.float32 else (1e-2, 2e-3)
+        for a, b, name in ((y, yr, "y"), (xd.grad, xr.grad, "dx"), (wd.grad, wr.grad, "dw")):
+            mx, mean = rel_errors(a.cpu(), b)
+            assert mx <= tol[0] and mean <= tol[1], f"{name}: {mx:.3e} {mean:.3e}"
+        for e, c in enumerate(counts):
+            if c == 0:
+                assert torch.count_nonzero(wd.grad[e]) == 0
+
+
+def test_grouped_matmul_integer_exact(hip_ops):
+    """Small-integer operands: every product and partial sum is exact in fp32."""
+    g = torch.Generator().manual_seed(11)
+    counts = [37, 0, 300, 99]
+    M, K, N = sum(counts), 256, 264
+    x = torch.randint(-3, 4, (M, K), generator=g).to(torch.bfloat16)
+    w = torch.randint(-3, 4, (4, K, N), generator=g).to(torch.bfloat16)
+    y = hip_ops.grouped_matmul(x.to(DEV), w.to(DEV), counts)
+    yr = o_gmm.grouped_matmul(x.double(), w.double(), counts)
+    assert torch.equal(y.cpu().double(), yr)
+
+
+# ---------------------------------------------------------------------------
+# FP8 block-scaled grouped GEMM
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("counts,K,N", [([0, 130, 7, 256], 256, 384), ([64, 64], 512, 256)])
+def test_grouped_matmul_fp8(hip_ops, counts, K, N):
+    g = torch.Generator().manual_seed(K + N)
+    E, M = len(counts), sum(counts)
+    master = torch.randn(E, N, K, generator=g) * 0.02
+    q, s = o_fp8.quantize_experts(master)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    dy = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    deq = o_fp8.dequantize_experts(q, s)
+    xr = x.double().requires_grad_()
+    wr = deq.double().requires_grad_()
+    yr = o_gmm.grouped_matmul(xr, wr, counts, trans_b=True)
+    yr.backward(dy.double())
+    xd = x.to(DEV).requires_grad_()
+    md = deq.to(DEV).requires_grad_()
+    y = hip_ops.grouped_matmul_fp8(xd, q.to(DEV), s.to(DEV), counts, master=md)
+    y.backward(dy.to(DEV))
+    for a, b, name in ((y, yr, "y"), (xd.grad, xr.grad, "dx"), (md.grad, wr.grad, "dw")):
+        mx, mean = rel_errors(a.cpu(), b)
+        assert mx <= 1e-2 and mean <= 2e-3, f"{name}: {mx:.3e} {mean:.3e}"
+
+
+def test_fp8_dequant_exact_through_gemm(hip_ops):
+    """x = unit rows selects single weight columns: y equals the dequantized weight bit-exactly."""
+    E, N, K = 2, 256, 256
+    g = torch.Generator().manual_seed(1)
+    master = torch.randn(E, N, K, generator=g) * 0.3
+    q, s = o_fp8.quantize_experts(master)
+    deq = o_fp8.dequantize_experts(q, s)
+    x = torch.eye(K).repeat(E, 1).to(torch.bfloat16)  # [E*K, K]
+    y = hip_ops.grouped_matmul_fp8(x.to(DEV), q.to(DEV), s.to(DEV), [K] * E)
+    expect = torch.cat([deq[e].t() for e in range(E)])  # row k of expert e = W[:, k]
+    assert torch.equal(y.cpu(), expect)

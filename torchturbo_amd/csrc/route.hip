@@ -1,0 +1,648 @@
+// Router top-k (fwd/bwd) and the deterministic routing index (counting sort).
+//
+// Router: one wave64 per token. Lane l owns the EPL consecutive experts
+// [l*EPL, (l+1)*EPL); top-k is k rounds of a wave arg-max (larger score
+// first, lower expert id on equal scores). Group-limited selection uses
+// segmented shuffles over the lanes of a group.
+//
+// Routing index: packed rows are ordered by expert, then token. Three kernels:
+//   hist  : per 256-token block, per-expert counts  -> bc[E][nb]
+//   scan  : per expert, exclusive scan over blocks   -> bc (in place), totals
+//   rank  : per block, expert base + wave prefix + in-wave ballot rank
+// The in-wave rank of a lane for expert e is popcount(ballot(lane has e) &
+// lanes below it), so the order is the token order and is reproducible.
+#include <math.h>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kRouterWaves = 4;  // tokens per 256-thread block
+
+struct Cand {
+  float sel;   // selection key (score, or score + bias)
+  int idx;     // expert id
+  float sc;    // score the probability is computed from
+  float lg;    // logit (fp32)
+};
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// Wave-wide arg-max (segment of `width` lanes when width < 64).
+__device__ __forceinline__ Cand cand_reduce(Cand c, int width) {
+  for (int off = width >> 1; off > 0; off >>= 1) {
+    Cand o;
+    o.sel = __shfl_xor(c.sel, off, TT_WAVE);
+    o.idx = __shfl_xor(c.idx, off, TT_WAVE);
+    o.sc = __shfl_xor(c.sc, off, TT_WAVE);
+    o.lg = __shfl_xor(c.lg, off, TT_WAVE);
+    if (better(o.sel, o.idx, c.sel, c.idx)) c = o;
+  }
+  return c;
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float softplus_f(float x) {
+  // PyTorch softplus with beta = 1, threshold = 20.
+  return x > 20.0f ? x : log1pf(expf(x));
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void router_fwd_kernel(
+    const void* __restrict__ logits, int ldt, int64_t T, int E, int K, int score_fn,
+    int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
+    const int64_t* __restrict__ fixed, void* __restrict__ probs, uint8_t* __restrict__ rmap,
+    int64_t* __restrict__ top_idx) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole wave; no block-level synchronisation below
+  const float NEG = -INFINITY;
+
+  float lg[EPL], sc[EPL], sel[EPL];
+  bool valid[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane * EPL + i;
+    valid[i] = e < E;
+    lg[i] = valid[i] ? load_as_f32(logits, ldt, t * E + e) : NEG;
+  }
+
+  // Scores.
+  if (score_fn == TT_SCORE_SOFTMAX) {
+    if (pre_softmax) {
+      float mx = NEG;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) mx = fmaxf(mx, lg[i]);
+      mx = wave_max(mx);
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        sc[i] = valid[i] ? expf(lg[i] - mx) : 0.f;
+        s += sc[i];
+      }
+      s = wave_sum(s);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) sc[i] = sc[i] / s;
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) sc[i] = lg[i];
+    }
+  } else if (score_fn == TT_SCORE_SIGMOID) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) sc[i] = valid[i] ? sigmoid_f(lg[i]) : 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) sc[i] = valid[i] ? sqrtf(softplus_f(lg[i])) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane * EPL + i;
+    float v = sc[i];
+    if (bias != nullptr && valid[i] && (score_fn != TT_SCORE_SOFTMAX || pre_softmax)) v = v + bias[e];
+    sel[i] = valid[i] ? v : NEG;
+  }
+
+  bool taken[EPL];
+  int slot[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    taken[i] = false;
+    slot[i] = 0;
+  }
+  Cand mine;  // lane j < K holds the j-th selected expert
+  mine.sel = NEG;
+  mine.idx = 0;
+  mine.sc = 0.f;
+  mine.lg = 0.f;
+
+  if (fixed != nullptr) {
+    // Token-id hash routing: ids are given; fetch their scores from owners.
+    int want = lane < K ? (int)fixed[t * K + lane] : -1;
+    if (want >= E) want = -1;
+    const int owner = want >= 0 ? want / EPL : 0;
+    const int part = want >= 0 ? want % EPL : 0;
+    float wsc = 0.f, wlg = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const float a = __shfl(sc[i], owner, TT_WAVE);
+      const float b = __shfl(lg[i], owner, TT_WAVE);
+      if (i == part) {
+        wsc = a;
+        wlg = b;
+      }
+    }
+    if (lane < K) {
+      mine.idx = want < 0 ? 0 : want;
+      mine.sc = wsc;
+      mine.lg = wlg;
+      mine.sel = 0.f;
+    }
+    for (int j = 0; j < K; ++j) {
+      const int id = __shfl(want, j, TT_WAVE);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (id == lane * EPL + i) {
+          taken[i] = true;
+          slot[i] = j;
+        }
+    }
+  } else {
+    if (GK > 0) {
+      // Group-limited: group score = sum of the top (K / GK) scores of the
+      // group; keep the GK best groups; mask the rest.
+      const int gs = E / G;        // experts per group
+      const int width = gs / EPL;  // lanes per group (power of two, checked)
+      const int m = K / GK;
+      bool used[EPL];
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) used[i] = false;
+      float gscore = 0.f;
+      for (int r = 0; r < m; ++r) {
+        Cand c;
+        c.sel = NEG;
+        c.idx = 0x7fffffff;
+        c.sc = 0.f;
+        c.lg = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          if (!used[i] && better(sel[i], lane * EPL + i, c.sel, c.idx)) {
+            c.sel = sel[i];
+            c.idx = lane * EPL + i;
+          }
+        c = cand_reduce(c, width);
+        gscore = gscore + c.sel;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          if (c.idx == lane * EPL + i) used[i] = true;
+      }
+      const int group = (lane * EPL) / gs;
+      const bool lane_live = lane * EPL < E;
+      bool keep = false;
+      float gkey = lane_live ? gscore : NEG;
+      for (int r = 0; r < GK; ++r) {
+        Cand c;
+        c.sel = keep ? NEG : gkey;
+        c.idx = lane_live ? group : 0x7fffffff;
+        c.sc = 0.f;
+        c.lg = 0.f;
+        c = cand_reduce(c, TT_WAVE);
+        if (c.idx == group) keep = true;
+      }
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (!keep) sel[i] = NEG;
+    }
+    for (int j = 0; j < K; ++j) {
+      Cand c;
+      c.sel = NEG;
+      c.idx = 0x7fffffff;
+      c.sc = 0.f;
+      c.lg = 0.f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (valid[i] && !taken[i] && better(sel[i], lane * EPL + i, c.sel, c.idx)) {
+          c.sel = sel[i];
+          c.idx = lane * EPL + i;
+          c.sc = sc[i];
+          c.lg = lg[i];
+        }
+      c = cand_reduce(c, TT_WAVE);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (c.idx == lane * EPL + i) {
+          taken[i] = true;
+          slot[i] = j;
+        }
+      if (lane == j) mine = c;
+    }
+  }
+
+  // Probabilities of the K selected experts (lanes 0..K-1), in fp32.
+  const bool active = lane < K;
+  float p;
+  if (score_fn == TT_SCORE_SOFTMAX && !pre_softmax) {
+    const float mx = wave_max(active ? mine.lg : NEG);
+    const float ex = active ? expf(mine.lg - mx) : 0.f;
+    const float s = wave_sum(ex);
+    p = ex / s;
+  } else if (score_fn == TT_SCORE_SOFTMAX) {
+    p = mine.sc;
+  } else {
+    const float s = wave_sum(active ? mine.sc : 0.f);
+    p = K > 1 ? mine.sc / (s + 1e-20f) : mine.sc;
+  }
+  if (scaling != 0.f) p = p * scaling;
+  p = round_to(p, ldt);
+
+  if (active) top_idx[t * K + lane] = mine.idx;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const float v = __shfl(p, slot[i], TT_WAVE);
+    if (valid[i]) {
+      const int64_t o = t * E + lane * EPL + i;
+      store_from_f32(probs, ldt, o, taken[i] ? v : 0.f);
+      rmap[o] = taken[i] ? 1 : 0;
+    }
+  }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void router_bwd_kernel(
+    const void* __restrict__ logits, int ldt, int64_t T, int E, int K, int score_fn,
+    int pre_softmax, float scaling, const int64_t* __restrict__ top_idx,
+    const void* __restrict__ grad, void* __restrict__ grad_logits) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float NEG = -INFINITY;
+  const bool active = lane < K;
+  int id = active ? (int)top_idx[t * K + lane] : 0;
+  if (id < 0 || id >= E) id = 0;
+  // d(probs) of the selected experts, as the fp32 gradient of the scaled probs.
+  float d = active ? load_as_f32(grad, ldt, t * E + id) : 0.f;
+  if (scaling != 0.f) d = d * scaling;
+  const float lgj = active ? load_as_f32(logits, ldt, t * E + id) : 0.f;
+
+  float out[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) out[i] = 0.f;
+
+  if (score_fn == TT_SCORE_SOFTMAX && pre_softmax) {
+    float lg[EPL], s[EPL], dv[EPL];
+    float mx = NEG;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane * EPL + i;
+      lg[i] = e < E ? load_as_f32(logits, ldt, t * E + e) : NEG;
+      mx = fmaxf(mx, lg[i]);
+      dv[i] = 0.f;
+    }
+    mx = wave_max(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      s[i] = (lane * EPL + i) < E ? expf(lg[i] - mx) : 0.f;
+      sum += s[i];
+    }
+    sum = wave_sum(sum);
+    for (int j = 0; j < K; ++j) {
+      const int e = __shfl(id, j, TT_WAVE);
+      const float g = __shfl(d, j, TT_WAVE);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (e == lane * EPL + i) dv[i] = g;
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      s[i] = s[i] / sum;
+      dot += s[i] * dv[i];
+    }
+    dot = wave_sum(dot);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) out[i] = s[i] * (dv[i] - dot);
+  } else {
+    float g;  // gradient w.r.t. the selected logit
+    if (score_fn == TT_SCORE_SOFTMAX) {
+      const float mx = wave_max(active ? lgj : NEG);
+      const float ex = active ? expf(lgj - mx) : 0.f;
+      const float p = ex / wave_sum(ex);
+      const float dot = wave_sum(active ? p * d : 0.f);
+      g = p * (d - dot);
+    } else {
+      float s, dsdx;
+      if (score_fn == TT_SCORE_SIGMOID) {
+        s = sigmoid_f(lgj);
+        dsdx = (1.0f - s) * s;
+      } else {
+        const float sp = softplus_f(lgj);
+        s = sqrtf(sp);
+        const float dsp = lgj > 20.0f ? 1.0f : sigmoid_f(lgj);
+        dsdx = dsp / (2.0f * s);
+      }
+      float ds = d;
+      if (K > 1) {
+        const float den = wave_sum(active ? s : 0.f) + 1e-20f;
+        const float dden = wave_sum(active ? -d * s / (den * den) : 0.f);
+        ds = d / den + dden;
+      }
+      g = ds * dsdx;
+    }
+    for (int j = 0; j < K; ++j) {
+      const int e = __shfl(id, j, TT_WAVE);
+      const float gj = __shfl(g, j, TT_WAVE);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (e == lane * EPL + i) out[i] = gj;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane * EPL + i;
+    if (e < E) store_from_f32(grad_logits, ldt, t * E + e, out[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Routing index.
+// ---------------------------------------------------------------------------
+constexpr int kIdxBlock = 256;  // tokens per block
+
+__global__ __launch_bounds__(kIdxBlock) void route_hist_kernel(
+    const int64_t* __restrict__ ids, int64_t T, int K, int E, int nb, int* __restrict__ bc) {
+  extern __shared__ int hist[];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+  __syncthreads();
+  const int64_t t = (int64_t)blockIdx.x * kIdxBlock + threadIdx.x;
+  if (t < T) {
+    for (int j = 0; j < K; ++j) {
+      const int64_t e = ids[t * K + j];
+      if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) bc[(int64_t)e * nb + blockIdx.x] = hist[e];
+}
+
+// One wave per expert: exclusive scan of its per-block counts, in place.
+__global__ __launch_bounds__(64) void route_scan_kernel(int* __restrict__ bc, int nb, int E,
+                                                        int* __restrict__ totals,
+                                                        int64_t* __restrict__ counts) {
+  const int e = blockIdx.x;
+  const int lane = threadIdx.x;
+  int* col = bc + (int64_t)e * nb;
+  int running = 0;
+  for (int base = 0; base < nb; base += TT_WAVE) {
+    const int i = base + lane;
+    const int c = i < nb ? col[i] : 0;
+    int incl = c;
+#pragma unroll
+    for (int off = 1; off < TT_WAVE; off <<= 1) {
+      const int o = __shfl_up(incl, off, TT_WAVE);
+      if (lane >= off) incl += o;
+    }
+    if (i < nb) col[i] = running + incl - c;
+    running += __shfl(incl, TT_WAVE - 1, TT_WAVE);
+  }
+  if (lane == 0) {
+    totals[e] = running;
+    counts[e] = running;
+  }
+}
+
+template <int KMAX>
+__global__ __launch_bounds__(kIdxBlock) void route_rank_kernel(
+    const int64_t* __restrict__ ids, int64_t T, int K, int E, int nb, const int* __restrict__ bc,
+    const int* __restrict__ totals, const void* __restrict__ probs, int pbytes,
+    int32_t* __restrict__ rows_out, int32_t* __restrict__ token_of_row,
+    void* __restrict__ packed_probs) {
+  extern __shared__ int smem[];
+  int* start = smem;           // [E]   first packed row of each expert
+  int* wbase = smem + E;       // [4][E] per-wave base row of each expert
+  __shared__ int wsum[kIdxBlock / TT_WAVE];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+
+  // Exclusive scan of the expert totals (each thread owns a run of experts).
+  const int per = (E + kIdxBlock - 1) / kIdxBlock;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < E) local += totals[e];
+  }
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < TT_WAVE; off <<= 1) {
+    const int o = __shfl_up(incl, off, TT_WAVE);
+    if (lane >= off) incl += o;
+  }
+  if (lane == TT_WAVE - 1) wsum[wave] = incl;
+  for (int e = tid; e < 4 * E; e += kIdxBlock) wbase[e] = 0;
+  __syncthreads();
+  int before = 0;
+  for (int w = 0; w < wave; ++w) before += wsum[w];
+  int run = before + incl - local;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < E) {
+      start[e] = run;
+      run += totals[e];
+    }
+  }
+
+  // Per-wave counts of this block.
+  const int64_t t = (int64_t)blockIdx.x * kIdxBlock + tid;
+  int my[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    my[j] = -1;
+    if (j < K && t < T) {
+      const int64_t e = ids[t * K + j];
+      my[j] = (e >= 0 && e < E) ? (int)e : -1;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j)
+    if (my[j] >= 0) atomicAdd(&wbase[wave * E + my[j]], 1);
+  __syncthreads();
+  // Turn per-wave counts into per-wave base rows.
+  for (int e = tid; e < E; e += kIdxBlock) {
+    int base = start[e] + bc[(int64_t)e * nb + blockIdx.x];
+    for (int w = 0; w < kIdxBlock / TT_WAVE; ++w) {
+      const int c = wbase[w * E + e];
+      wbase[w * E + e] = base;
+      base += c;
+    }
+  }
+  __syncthreads();
+
+  // In-wave stable rank: one ballot per expert present in the wave.
+  int row[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) row[j] = -1;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (TT_WAVE - lane));
+  for (int e = 0; e < E; ++e) {
+    int slot = -1;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      if (my[j] == e) slot = j;
+    const uint64_t mask = __ballot(slot >= 0);
+    if (mask == 0) continue;  // uniform across the wave
+    if (slot >= 0) {
+      const int r = wbase[wave * E + e] + __popcll(mask & below);
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (j == slot) row[j] = r;
+    }
+  }
+  if (t < T) {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j >= K) break;
+      const int r = row[j];
+      rows_out[t * K + j] = r;
+      if (r >= 0) {
+        token_of_row[r] = (int32_t)t;
+        if (probs != nullptr && packed_probs != nullptr) {
+          const int64_t src = t * E + my[j];
+          if (pbytes == 4)
+            static_cast<uint32_t*>(packed_probs)[r] = static_cast<const uint32_t*>(probs)[src];
+          else
+            static_cast<uint16_t*>(packed_probs)[r] = static_cast<const uint16_t*>(probs)[src];
+        }
+      }
+    }
+  }
+}
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+template <int EPL>
+void launch_router_fwd(dim3 g, hipStream_t s, const void* logits, int ldt, int64_t T, int E, int K,
+                       int sf, int pre, const float* bias, int G, int GK, float scale,
+                       const int64_t* fixed, void* probs, uint8_t* rmap, int64_t* top) {
+  hipLaunchKernelGGL(router_fwd_kernel<EPL>, g, dim3(256), 0, s, logits, ldt, T, E, K, sf, pre,
+                     bias, G, GK, scale, fixed, probs, rmap, top);
+}
+
+template <int EPL>
+void launch_router_bwd(dim3 g, hipStream_t s, const void* logits, int ldt, int64_t T, int E, int K,
+                       int sf, int pre, float scale, const int64_t* top, const void* grad,
+                       void* gl) {
+  hipLaunchKernelGGL(router_bwd_kernel<EPL>, g, dim3(256), 0, s, logits, ldt, T, E, K, sf, pre,
+                     scale, top, grad, gl);
+}
+
+int epl_for(int E) {
+  const int need = (E + TT_WAVE - 1) / TT_WAVE;
+  int epl = 1;
+  while (epl < need) epl <<= 1;
+  return epl;
+}
+
+bool float_dtype(int d) { return d == TT_F32 || d == TT_BF16 || d == TT_F16; }
+
+}  // namespace
+
+extern "C" int tt_router_topk_fwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                                  int32_t num_experts, int32_t topk, int32_t score_function,
+                                  int32_t pre_softmax, const float* expert_bias,
+                                  int32_t num_groups, int32_t group_topk, float scaling_factor,
+                                  const int64_t* fixed_indices, void* probs,
+                                  uint8_t* routing_map, int64_t* top_indices, void* stream) {
+  TT_REQUIRE(float_dtype(logits_dtype), "router: unsupported logits dtype %d", logits_dtype);
+  TT_REQUIRE(num_tokens >= 0, "router: negative token count");
+  TT_REQUIRE(num_experts >= 1 && num_experts <= 1024, "router: num_experts must be in [1, 1024]");
+  TT_REQUIRE(topk >= 1 && topk <= 64 && topk <= num_experts, "router: topk must be in [1, min(64, E)]");
+  TT_REQUIRE(score_function >= 0 && score_function <= 2, "router: bad score function");
+  const int epl = epl_for(num_experts);
+  if (group_topk > 0 && fixed_indices == nullptr) {
+    TT_REQUIRE(num_groups > 0 && num_experts % num_groups == 0,
+               "router: num_experts must be divisible by num_groups");
+    TT_REQUIRE(group_topk <= num_groups && topk % group_topk == 0,
+               "router: topk must be divisible by group_topk <= num_groups");
+    const int gs = num_experts / num_groups;
+    const int width = gs / epl;
+    TT_REQUIRE(gs % epl == 0 && width >= 1 && (width & (width - 1)) == 0 && TT_WAVE % width == 0,
+               "router: group size %d does not map onto whole lanes (%d experts per lane)", gs, epl);
+    TT_REQUIRE(topk / group_topk <= gs, "router: topk / group_topk exceeds the group size");
+    TT_REQUIRE(topk <= group_topk * gs, "router: topk exceeds the experts of the kept groups");
+  }
+  if (num_tokens == 0) return TT_OK;
+  const dim3 grid((unsigned)((num_tokens + kRouterWaves - 1) / kRouterWaves));
+  const int gk = fixed_indices ? 0 : group_topk;
+  switch (epl) {
+#define TT_CASE(N)                                                                               \
+  case N:                                                                                        \
+    launch_router_fwd<N>(grid, S(stream), logits, logits_dtype, num_tokens, num_experts, topk,   \
+                         score_function, pre_softmax, expert_bias, num_groups, gk,              \
+                         scaling_factor, fixed_indices, probs, routing_map, top_indices);        \
+    break;
+    TT_CASE(1) TT_CASE(2) TT_CASE(4) TT_CASE(8) TT_CASE(16)
+#undef TT_CASE
+    default:
+      tt_set_error("router: unsupported expert count");
+      return TT_ERR_UNSUPPORTED;
+  }
+  return tt_check_launch("router_fwd");
+}
+
+extern "C" int tt_router_topk_bwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                                  int32_t num_experts, int32_t topk, int32_t score_function,
+                                  int32_t pre_softmax, float scaling_factor,
+                                  const int64_t* top_indices, const void* grad_probs,
+                                  void* grad_logits, void* stream) {
+  TT_REQUIRE(float_dtype(logits_dtype), "router_bwd: unsupported logits dtype %d", logits_dtype);
+  TT_REQUIRE(num_experts >= 1 && num_experts <= 1024, "router_bwd: num_experts must be in [1, 1024]");
+  TT_REQUIRE(topk >= 1 && topk <= 64 && topk <= num_experts, "router_bwd: bad topk");
+  TT_REQUIRE(score_function >= 0 && score_function <= 2, "router_bwd: bad score function");
+  if (num_tokens == 0) return TT_OK;
+  const dim3 grid((unsigned)((num_tokens + kRouterWaves - 1) / kRouterWaves));
+  switch (epl_for(num_experts)) {
+#define TT_CASE(N)                                                                            \
+  case N:                                                                                     \
+    launch_router_bwd<N>(grid, S(stream), logits, logits_dtype, num_tokens, num_experts, topk, \
+                         score_function, pre_softmax, scaling_factor, top_indices, grad_probs, \
+                         grad_logits);                                                        \
+    break;
+    TT_CASE(1) TT_CASE(2) TT_CASE(4) TT_CASE(8) TT_CASE(16)
+#undef TT_CASE
+    default:
+      tt_set_error("router_bwd: unsupported expert count");
+      return TT_ERR_UNSUPPORTED;
+  }
+  return tt_check_launch("router_bwd");
+}
+
+extern "C" size_t tt_route_index_workspace(int64_t num_tokens, int32_t num_experts) {
+  const int64_t nb = (num_tokens + kIdxBlock - 1) / kIdxBlock;
+  return (size_t)(nb * num_experts + num_experts) * sizeof(int) + 256;
+}
+
+extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
+                              int32_t num_experts, const void* probs_dense, int probs_dtype,
+                              int32_t* row_indices, int32_t* token_of_row, void* packed_probs,
+                              int64_t* tokens_per_expert, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  TT_REQUIRE(num_tokens >= 0 && num_tokens * (int64_t)topk < (1ll << 31),
+             "route_index: T * k must fit in int32");
+  TT_REQUIRE(num_experts >= 1 && num_experts <= 2048, "route_index: num_experts must be in [1, 2048]");
+  TT_REQUIRE(topk >= 1 && topk <= 64, "route_index: topk must be in [1, 64]");
+  TT_REQUIRE(workspace_bytes >= tt_route_index_workspace(num_tokens, num_experts),
+             "route_index: workspace too small");
+  if (probs_dense != nullptr && packed_probs != nullptr)
+    TT_REQUIRE(float_dtype(probs_dtype), "route_index: unsupported probs dtype %d", probs_dtype);
+  hipStream_t s = S(stream);
+  const int nb = (int)((num_tokens + kIdxBlock - 1) / kIdxBlock);
+  int* bc = static_cast<int*>(workspace);
+  int* totals = bc + (int64_t)nb * num_experts;
+  if (num_tokens == 0) {
+    // Counts are all zero; a one-wave scan over zero blocks writes them.
+    hipLaunchKernelGGL(route_scan_kernel, dim3(num_experts), dim3(64), 0, s, bc, 0, num_experts,
+                       totals, tokens_per_expert);
+    return tt_check_launch("route_scan");
+  }
+  hipLaunchKernelGGL(route_hist_kernel, dim3(nb), dim3(kIdxBlock), num_experts * sizeof(int), s,
+                     expert_indices, num_tokens, topk, num_experts, nb, bc);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(num_experts), dim3(64), 0, s, bc, nb, num_experts,
+                     totals, tokens_per_expert);
+  const size_t lds = (size_t)5 * num_experts * sizeof(int);
+  TT_REQUIRE(lds <= 160 * 1024 - 64, "route_index: too many experts for LDS");
+  const int pbytes = tt_elem_size(probs_dtype);
+  const void* pd = (packed_probs != nullptr) ? probs_dense : nullptr;
+#define TT_RANK(KM)                                                                               \
+  hipLaunchKernelGGL(route_rank_kernel<KM>, dim3(nb), dim3(kIdxBlock), lds, s, expert_indices,    \
+                     num_tokens, topk, num_experts, nb, bc, totals, pd, pbytes, row_indices,      \
+                     token_of_row, packed_probs)
+  if (topk <= 2) TT_RANK(2);
+  else if (topk <= 4) TT_RANK(4);
+  else if (topk <= 8) TT_RANK(8);
+  else if (topk <= 16) TT_RANK(16);
+  else TT_RANK(64);
+#undef TT_RANK
+  return tt_check_launch("route_rank");
+}

@@ -1,0 +1,239 @@
+"""Top-k router.
+
+Mirrors ``TopKRouter`` (``src/torchturbo/models/modules/moe/router.py:25-380``):
+the gating linear runs in the router dtype with autocast off and recomputes
+its casts in backward (``:25-58``); ``routing`` applies the z-loss, calls the
+top-k selection, attaches the aux loss and accumulates expert-bias counts
+(``:277-356``). Top-k selection goes through the ``topk_softmax_with_capacity``
+op so the GPU runs the fused HIP router kernel; the aux/z-loss statistics
+stay in PyTorch, as in the reference.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.distributed as dist
+
+from ..dispatch import ops
+from .moe_config import MoEConfig
+
+
+def _group_size(group) -> int:
+    if group is None or not dist.is_available() or not dist.is_initialized():
+        return 1
+    return dist.get_world_size(group)
+
+
+class MoEAuxLossAutoScaler(torch.autograd.Function):
+    """Attach an auxiliary loss to an activation (``moe_utils.py:73-90``)."""
+
+    loss_scale = 1.0
+
+    @staticmethod
+    def forward(ctx, output, aux_loss):
+        ctx.save_for_backward(aux_loss)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (aux_loss,) = ctx.saved_tensors
+        return grad_output, torch.ones_like(aux_loss) * MoEAuxLossAutoScaler.loss_scale
+
+    @classmethod
+    def set_loss_scale(cls, scale: float) -> None:
+        cls.loss_scale = scale
+
+
+def mask_padding_tokens(values, padding_mask):
+    if padding_mask is None:
+        return values
+    return values * (~padding_mask.reshape(-1).bool()).unsqueeze(-1)
+
+
+def compute_routing_scores_for_aux_loss(logits, topk, score_function, padding_mask=None):
+    """Bias-free routing map and scores for the aux loss (``moe_utils.py:15-45``)."""
+    logits = logits.reshape(-1, logits.size(-1))
+    if score_function == "softmax":
+        scores = torch.softmax(logits, dim=-1, dtype=torch.float32)
+    elif score_function in ("sigmoid", "sqrtsoftplus"):
+        scores = (torch.sigmoid(logits.float()) if score_function == "sigmoid"
+                  else torch.nn.functional.softplus(logits.float()).sqrt())
+        scores = scores / (scores.sum(dim=-1, keepdim=True) + 1e-20)
+    else:
+        raise ValueError(f"Invalid score_function: {score_function}")
+    top = torch.topk(scores, k=topk, dim=-1).indices
+    routing_map = torch.zeros_like(logits, dtype=torch.int32).scatter_(1, top, 1).bool()
+    if padding_mask is not None:
+        scores = mask_padding_tokens(scores, padding_mask)
+        routing_map = mask_padding_tokens(routing_map, padding_mask).bool()
+    return routing_map, scores
+
+
+def z_loss_func(logits, z_loss_coeff, padding_mask=None):
+    """Mean squared logsumexp over valid tokens (``moe_utils.py:48-70``)."""
+    values = torch.square(torch.logsumexp(logits, dim=-1))
+    if padding_mask is not None:
+        valid = ~padding_mask.reshape(-1).bool()
+        z = (values * valid).sum() / torch.clamp(valid.sum(), min=1)
+    else:
+        z = values.sum() if logits.shape[0] == 0 else values.mean()
+    return z * z_loss_coeff
+
+
+class RouterGatingLinearFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, input, weight, router_dtype):
+        ctx.save_for_backward(input, weight)
+        ctx.router_dtype = router_dtype
+        with torch.autocast(device_type=input.device.type, enabled=False):
+            return torch.nn.functional.linear(input.to(router_dtype), weight.to(router_dtype))
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        input, weight = ctx.saved_tensors
+        grad_output = grad_output.reshape(-1, grad_output.shape[-1])
+        grad_input = grad_weight = None
+        if ctx.needs_input_grad[0]:
+            grad_input = grad_output.mm(weight.to(ctx.router_dtype))
+            grad_input = grad_input.view(input.shape).to(input.dtype)
+        if ctx.needs_input_grad[1]:
+            flat = input.reshape(-1, input.shape[-1]).to(ctx.router_dtype)
+            grad_weight = grad_output.t().mm(flat).to(weight.dtype)
+        return grad_input, grad_weight, None
+
+
+class Router(torch.nn.Module):
+    def __init__(self, config: MoEConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.num_experts = config.num_moe_experts
+        self.layer_number = None
+        self.weight = torch.nn.Parameter(
+            torch.empty((config.num_moe_experts, config.hidden_size), dtype=torch.float32)
+        )
+        if config.perform_initialization:
+            config.init_method(self.weight)
+        self.weight.data = self.weight.data.to(dtype=config.params_dtype)
+
+    def router_dtype(self, input_dtype):
+        if self.config.moe_router_dtype == "fp32":
+            return torch.float32
+        if self.config.moe_router_dtype == "fp64":
+            return torch.float64
+        return input_dtype
+
+    def gating(self, input):
+        if self.weight.device != input.device:
+            self.weight.data = self.weight.data.to(device=input.device)
+        return RouterGatingLinearFunction.apply(input, self.weight, self.router_dtype(input.dtype))
+
+
+class TopKRouter(Router):
+    def __init__(self, config: MoEConfig, layer_number: Optional[int] = None, sp_group=None):
+        super().__init__(config=config)
+        self.topk = config.moe_router_topk
+        self.routing_type = config.moe_router_load_balancing_type
+        self.score_function = config.moe_router_score_function
+        self.layer_number = layer_number
+        self.sp_group = sp_group
+        self._metrics = None
+        self.use_hash_routing = (layer_number is not None and layer_number < config.num_hash_layers
+                                 and config.vocab_size > 0)
+        self.enable_expert_bias = config.moe_router_enable_expert_bias and not self.use_hash_routing
+        if self.enable_expert_bias:
+            self.register_buffer("expert_bias",
+                                 torch.zeros(config.num_moe_experts, dtype=torch.float32))
+        else:
+            self.expert_bias = None
+        if self.use_hash_routing:
+            self.register_buffer("tid2eid", torch.stack([
+                torch.randperm(config.num_moe_experts)[: self.topk]
+                for _ in range(config.vocab_size)
+            ]).long())
+
+    def _maintain_float32_expert_bias(self):
+        if getattr(self, "expert_bias", None) is not None and self.expert_bias.dtype != torch.float32:
+            self.expert_bias.data = self.expert_bias.data.to(torch.float32)
+
+    def _apply_aux_loss(self, probs, scores, routing_map):
+        coeff = self.config.moe_aux_loss_coeff
+        if coeff == 0.0:
+            return probs
+        tokens_per_expert = routing_map.sum(dim=0)
+        sp_size = _group_size(self.sp_group)
+        if sp_size > 1:
+            dist.all_reduce(tokens_per_expert, op=dist.ReduceOp.SUM, group=self.sp_group)
+        total = (tokens_per_expert.sum() / self.topk).clamp_min(1)
+        raw = (torch.sum(scores.sum(dim=0) * tokens_per_expert) * self.num_experts * sp_size
+               / (self.topk * total * total))
+        aux = raw * coeff
+        self._metrics = {**(self._metrics or {}), "aux_loss": (aux / coeff).detach(),
+                         "aux_loss_scaled": aux.detach()}
+        return MoEAuxLossAutoScaler.apply(probs, aux)
+
+    def apply_z_loss(self, logits, padding_mask=None):
+        coeff = self.config.moe_z_loss_coeff
+        if not coeff or not (self.training and torch.is_grad_enabled()):
+            return logits
+        if padding_mask is not None:
+            local = (~padding_mask.reshape(-1).bool()).sum()
+        else:
+            local = torch.tensor(logits.shape[0], device=logits.device, dtype=torch.long)
+        total = local.clone()
+        sp_size = _group_size(self.sp_group)
+        if sp_size > 1:
+            dist.all_reduce(total, op=dist.ReduceOp.SUM, group=self.sp_group)
+        z = z_loss_func(logits, coeff, padding_mask) * (sp_size * local / torch.clamp(total, min=1))
+        self._metrics = {**(self._metrics or {}), "z_loss": (z / coeff).detach(),
+                         "z_loss_scaled": z.detach()}
+        return MoEAuxLossAutoScaler.apply(logits, z)
+
+    def pop_metrics(self):
+        metrics = self._metrics or {}
+        self._metrics = None
+        return metrics
+
+    def routing(self, logits, input_ids=None, padding_mask=None,
+                accumulate_tokens_per_expert: bool = True):
+        logits = logits.view(-1, self.config.num_moe_experts)
+        input_ids = input_ids.view(-1) if input_ids is not None else None
+        if self.use_hash_routing and input_ids is None:
+            raise ValueError("Hash routing requires input_ids.")
+        logits = self.apply_z_loss(logits, padding_mask=padding_mask)
+        if self.routing_type != "none":
+            raise ValueError(f"Unsupported MoE routing type: {self.routing_type}")
+        probs, routing_map, expert_indices = ops.topk_softmax_with_capacity(
+            logits, self.topk,
+            use_pre_softmax=self.config.moe_router_pre_softmax,
+            num_groups=self.config.moe_router_num_groups,
+            group_topk=self.config.moe_router_group_topk,
+            scaling_factor=self.config.moe_router_topk_scaling_factor,
+            score_function=self.score_function,
+            expert_bias=self.expert_bias,
+            use_hash_routing=self.use_hash_routing,
+            hash_table=getattr(self, "tid2eid", None),
+            input_ids=input_ids,
+        )
+        if (self.training and torch.is_grad_enabled() and not self.use_hash_routing
+                and self.config.moe_aux_loss_coeff > 0.0):
+            aux_map, aux_scores = compute_routing_scores_for_aux_loss(
+                logits, self.topk, self.score_function, padding_mask)
+            probs = self._apply_aux_loss(probs, aux_scores, aux_map)
+        if self.enable_expert_bias and accumulate_tokens_per_expert and torch.is_grad_enabled():
+            with torch.no_grad():
+                counts = mask_padding_tokens(routing_map, padding_mask).sum(dim=0).to(torch.float32)
+                if not hasattr(self, "local_tokens_per_expert"):
+                    self.register_buffer("local_tokens_per_expert", torch.zeros_like(counts),
+                                         persistent=False)
+                self.local_tokens_per_expert.add_(counts)
+        return probs, routing_map, expert_indices
+
+    def forward(self, input, input_ids=None, padding_mask=None,
+                accumulate_tokens_per_expert: bool = True):
+        self._maintain_float32_expert_bias()
+        logits = self.gating(input)
+        probs, routing_map, expert_indices = self.routing(
+            logits, input_ids, padding_mask, accumulate_tokens_per_expert)
+        return probs, routing_map, expert_indices, logits

@@ -1,0 +1,41 @@
+"""HIP top-k router provider.
+
+Implements ``topk_softmax_with_capacity``
+(``src/torchturbo/models/modules/moe/utils.py:127-230``) in one kernel per
+direction: score function, optional expert bias (selection only),
+group-limited selection, top-k, normalisation, scaling, the cast to the
+logits dtype and the dense probs / boolean map, with its autograd backward.
+Ties between equal scores go to the lower expert id.
+"""
+
+from __future__ import annotations
+
+from ...dispatch import OpImpl, OpImplKind, register_op
+from ...runtime import TurboDevice
+from . import PRIORITY
+from ._functions import TopKRouting, require_cuda
+from .available import hip_available
+
+
+@register_op(op_name="topk_softmax_with_capacity", impl_name="hip_topk_softmax",
+             kind=OpImplKind.CUSTOM, priority=PRIORITY, devices=(TurboDevice.CUDA,))
+class HipTopKSoftmax(OpImpl):
+    def available(self) -> bool:
+        return hip_available()
+
+    def __call__(self, logits, topk, use_pre_softmax=False, num_groups=None, group_topk=None,
+                 scaling_factor=None, score_function="softmax", expert_bias=None,
+                 use_hash_routing=False, hash_table=None, input_ids=None):
+        require_cuda(logits)
+        if logits.dim() != 2:
+            raise ValueError(f"Expected 2D logits [num_tokens, num_experts], got {logits.dim()}.")
+        if score_function not in ("softmax", "sigmoid", "sqrtsoftplus"):
+            raise ValueError(f"Invalid score_function: {score_function}")
+        fixed = None
+        if use_hash_routing:
+            if hash_table is None or input_ids is None:
+                raise ValueError("Hash routing requires hash_table and input_ids.")
+            fixed = hash_table.to(logits.device)[input_ids.to(logits.device)]
+        bias = expert_bias if score_function != "softmax" or use_pre_softmax else None
+        return TopKRouting.apply(logits, int(topk), score_function, bool(use_pre_softmax),
+                                 num_groups, group_topk, scaling_factor, bias, fixed)
