@@ -606,16 +606,19 @@ int launch_mfma(const void* p0, const void* p1, const void* scale, int sdt, void
   TT_REQUIRE(nblk < 0x7fffffff, "gmm: grid too large");
   const size_t lds = lds_bytes<C>(E);
   TT_REQUIRE(lds <= 160 * 1024, "gmm: too many experts for the LDS tile schedule");
-  static bool lds_attr = false;  // per instantiation; the call is idempotent
-  if (!lds_attr) {
+  // Dynamic LDS above 64 KiB must be allowed per kernel; raise the limit to
+  // what this launch needs (kept per instantiation, only ever increased).
+  static size_t lds_allowed = 64 * 1024;
+  if (lds > lds_allowed) {
     const hipError_t err = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&gmm_kernel<C, MODE, TB, FP8, ET>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (err != hipSuccess) {
-      tt_set_error("gmm: hipFuncSetAttribute: %s", hipGetErrorString(err));
+      (void)hipGetLastError();  // do not leave the error for the next launch check
+      tt_set_error("gmm: hipFuncSetAttribute(%zu bytes): %s", lds, hipGetErrorString(err));
       return TT_ERR_HIP;
     }
-    lds_attr = true;
+    lds_allowed = lds;
   }
   hipLaunchKernelGGL((gmm_kernel<C, MODE, TB, FP8, ET>), dim3((unsigned)nblk), dim3(C::NT), lds, s,
                      static_cast<const char*>(p0), static_cast<const char*>(p1),
