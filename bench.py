@@ -41,7 +41,38 @@ def parse():
     p.add_argument("--workload", default="qwen3_30b_a3b")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                   help="only run a plain device-to-device copy of BYTES bytes "
+                        "(the reference kernel that scales the FETCH_SIZE / WRITE_SIZE "
+                        "counters to bytes)")
     return p.parse_args()
+
+
+def copy_calibration(nbytes, launches=4):
+    """A copy of known size: each launch reads and writes exactly ``nbytes``."""
+    dev = torch.device("cuda", 0)
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes": nbytes, "launches": launches}), flush=True)
+
+
+def measured_traffic(workload):
+    """HBM bytes per grouped-GEMM launch from the committed counter summary
+    ``profiles/gmm_traffic_<workload>.txt`` (line ``bytes_per_launch: N``),
+    or None when no such summary exists."""
+    path = os.path.join(ROOT, "profiles", f"gmm_traffic_{workload}.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def build_layer(w, device):
@@ -189,6 +220,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU (EP=1); --gpus must be 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     from torchturbo_amd import configs as C
 
     w = C.resolve(C.WORKLOADS[args.workload])
@@ -234,7 +268,8 @@ def main():
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(w.name),
+            "traffic_unit": "bytes/launch",
             "launches": gemm_launches,
             "avg_launch_us": round(avg_launch_s * 1e6, 1),
             "gemm_ms_per_step": round(gemm_ms / args.steps, 3),

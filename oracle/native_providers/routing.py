@@ -18,8 +18,10 @@ Restates ``topk_softmax_with_capacity`` and ``group_limited_topk`` of
 
 Ties: PyTorch's CPU ``topk`` has no documented tie rule. The HIP router
 breaks ties toward the lower expert id; inputs used for bit-exact routing
-comparisons use fp32 logits, where ties have measure zero, and the tie rule
-itself is pinned by ``tests/test_router_ties.py`` on the CPU.
+comparisons use fp32 logits, where ties have measure zero (low-precision
+comparisons skip rows whose k-th and (k+1)-th scores are equal), and the HIP
+tie rule has its own test (``tests/test_gpu_ops.py``,
+``test_router_ties_go_to_lower_expert``).
 
 Pinned by: the KATs of ``tests/models/test_moe_router.py:74-171`` and
 ``tests/models/test_moe_adapter_routing.py:179-243`` restated in
