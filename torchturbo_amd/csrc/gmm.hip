@@ -10,15 +10,18 @@
 //
 // Two kernels share the tile schedule:
 //
-// * gmm_dma_kernel (bf16/f16): 256x256x32 block tiles, 8 waves of 128x64,
-//   four LDS stages filled by direct global->LDS loads (global_load_lds,
-//   16 bytes per lane, no register round trip), three k-tiles in flight.
-//   K-major tiles are stored [row][k] with the 16-byte chunks of a row
-//   XOR-swizzled, read with ds_read_b128. MN-major tiles are stored in their
-//   natural [k][row] order (swizzled) and read with the gfx950 transposing
-//   LDS load ds_read_b64_tr_b16, which hands each lane four consecutive k of
-//   one column: no register transpose. Out-of-range chunks load from a zero
-//   line, so no lane ever reads outside its operand.
+// * gmm_mfma_kernel (bf16/f16): 256x256x32 block tiles, 4 waves of 128x128
+//   (one wave per SIMD, 256 accumulator registers). Operands stream into
+//   four LDS stages with buffer loads that write LDS directly (16 bytes per
+//   lane, no register round trip); three k-tiles are in flight. Each buffer
+//   resource spans exactly its operand, so the hardware returns zeros past
+//   an expert's rows or reduction length and no lane reads outside its
+//   operand. K-major tiles are read with XOR-swizzled ds_read_b128;
+//   MN-major tiles keep their natural [k][row] order and are read with the
+//   gfx950 transposing load ds_read_b64_tr_b16 (no register transpose).
+//   MFMAs, fragment reads of the next k-step and DMA issue are interleaved
+//   one per slot. The epilogue converts to 16 bits in hardware and stores
+//   through LDS as full 256-byte rows.
 // * gmm_reg_kernel: 256x256x64 tiles through registers and two LDS stages,
 //   8x8 register transposes for MN-major operands. Used for FP8 weights: the
 //   e4m3 bytes are decoded and multiplied by their 128x128 block scale while
@@ -287,129 +290,46 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[FM][FN], const Ti
 }
 
 // ===========================================================================
-// DMA-pipelined kernel (bf16 / f16).
+// MFMA kernel (bf16 / f16): 256x256x32 block tiles, 4 waves of 128x128.
 // ===========================================================================
-constexpr int DM_BM = 256, DM_BN = 256, DM_BK = 32, DM_ST = 4, DM_NT = 512;
+constexpr int DM_BM = 256, DM_BN = 256, DM_BK = 32, DM_ST = 4, DM_NT = 256;
 constexpr int DM_TILE = DM_BM * DM_BK * 2;  // bytes of one operand tile (16 KiB)
 constexpr int DM_STAGE = 2 * DM_TILE;       // A tile then B tile
+constexpr uint32_t DM_OOB = 0xFFFFFFF0u;    // buffer offset past any resource
 
-// Source of out-of-range chunks: one zero line (read only).
-__device__ __align__(64) uint4 g_zero_line[4];
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 
-// One 16-byte global->LDS load per lane into lds_dst + 16 * lane (lds_dst is
-// wave-uniform; it goes to M0). Issued as inline assembly so the compiler
-// does not drain every outstanding DMA before each LDS read: completion of a
-// stage is awaited explicitly (TT_WAIT_VMCNT) before the barrier that
-// publishes it. Vector-memory results return in order, so the compiler's own
-// vmcnt waits for its loads stay sufficient. Nothing else in these kernels
-// uses M0.
-__device__ __forceinline__ void dma16(const void* src, char* lds_dst) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)lds_dst)));  // LDS offset
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+// Buffer resource over [base, base + bytes): offsets at or past `bytes` read
+// as zeros. Word 3 is the raw 32-bit data format of the gfx9 family.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, int64_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t n = bytes <= 0 ? 0u : (bytes < (int64_t)DM_OOB ? (uint32_t)bytes : DM_OOB);
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xFFFFu));
+  r.z = __builtin_amdgcn_readfirstlane((int)n);
+  r.w = 0x00020000;
+  return r;
+}
+
+// One 16-byte buffer load per lane straight into LDS at lds_addr + 16 * lane
+// (lds_addr is wave-uniform and goes to M0). Inline assembly, so that the
+// compiler does not drain outstanding loads before every LDS read:
+// completion of a stage is awaited explicitly (TT_WAIT_VMCNT) before the
+// barrier that publishes it. Nothing else in these kernels uses M0.
+__device__ __forceinline__ void dma16(uint32_t voff, i32x4 rsrc, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(m0), "v"(src)
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
                : "memory");
 }
 
-// Where each lane's four 16-byte DMA chunks of a k-tile come from. Built
-// once per block; per k-tile only the byte step and the k bound change, so a
-// single small set of registers stays live in the main loop.
-struct DmaPlan {
-  const char* src[4];  // chunk addresses at k-tile 0
-  int koff[4];         // k of the chunk relative to the k-tile start
-  bool ok[4];          // row / column inside the operand
-  int64_t step;        // bytes from one k-tile to the next
-  int dst;             // byte offset of the operand tile within a stage
-};
-
-// K-major tile: rows [row0, row0 + 256) x k [k0, k0 + 32); element (r, k)
-// at base + (r * ld + k) * 2. LDS row r occupies 64 bytes; its 16-byte chunk
-// c (k = 8c .. 8c + 7) sits in slot c ^ ((r >> 2) & 3), which keeps the
-// MFMA-operand reads (32 rows, one chunk) free of bank conflicts. A wave
-// writes 1 KiB (16 rows) per instruction, lane l to slot l & 3 of row l >> 2.
-__device__ __forceinline__ DmaPlan plan_kmajor(const char* base, int64_t ld, int64_t row0,
-                                               int64_t rows_valid, int dst, int wv, int lane) {
-  DmaPlan p;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int u = wv * 4 + q;
-    const int r = 16 * u + (lane >> 2);
-    const int c = (lane & 3) ^ ((r >> 2) & 3);
-    const int64_t gr = row0 + r;
-    p.ok[q] = gr < rows_valid;
-    p.koff[q] = 8 * c;
-    p.src[q] = base + (gr * ld + 8 * c) * 2;
-  }
-  p.step = (int64_t)DM_BK * 2;
-  p.dst = dst;
-  return p;
-}
-
-// MN-major tile: k rows [k0, k0 + 32) x columns [col0, col0 + 256); element
-// (k, c) at base + (k * ld + c) * 2. LDS k-row kr occupies 512 bytes; its
-// 16-byte chunk c (columns 8c .. 8c + 7) sits in slot c ^ (4 * (kr & 3)). A
-// wave writes two k-rows per instruction.
-__device__ __forceinline__ DmaPlan plan_mnmajor(const char* base, int64_t ld, int64_t col0,
-                                                int64_t cols_valid, int dst, int wv, int lane) {
-  DmaPlan p;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int u = wv * 4 + q;
-    const int kr = 2 * u + (lane >> 5);
-    const int c = (lane & 31) ^ (4 * (kr & 3));
-    const int64_t gc = col0 + 8 * c;
-    p.ok[q] = gc < cols_valid;
-    p.koff[q] = kr;
-    p.src[q] = base + (kr * ld + gc) * 2;
-  }
-  p.step = (int64_t)DM_BK * ld * 2;
-  p.dst = dst;
-  return p;
-}
-
-// Issue the lane's four chunks of k-tile kt into a stage; chunks outside the
-// operand (or past the reduction length) load from the zero line.
-__device__ __forceinline__ void dma_issue(const DmaPlan& p, char* stage, int kt, int64_t kvalid,
-                                          int wv) {
-  const int64_t k0 = (int64_t)kt * DM_BK;
-  const int64_t off = (int64_t)kt * p.step;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const void* src = (p.ok[q] && k0 + p.koff[q] < kvalid)
-                          ? static_cast<const void*>(p.src[q] + off)
-                          : static_cast<const void*>(g_zero_line);
-    dma16(src, stage + p.dst + (wv * 4 + q) * 1024);
-  }
-}
-
-// MFMA operand from a K-major tile: rows r0 .. r0 + 31, k-step s (16 k).
-__device__ __forceinline__ uint4 frag_k(const char* tile, int r0, int s, int lane) {
-  const int r = r0 + (lane & 31);
-  const int c = 2 * s + (lane >> 5);
-  return *reinterpret_cast<const uint4*>(tile + r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
-}
-
-// MFMA operand from an MN-major tile: columns c0 .. c0 + 31, k-step s. Two
-// transposing reads: within each 16-lane group, source lane i reads k-row
-// k + i / 4, columns col + 4 * (i % 4) .. + 3, and lane i receives column
-// col + i at the four k-rows.
-__device__ __forceinline__ uint4 frag_mn(const char* tile, int c0, int s, int lane) {
-  const int g = lane >> 4, i = lane & 15;
-  const int col = c0 + 16 * (g & 1) + 4 * (i & 3);
-  const int chunk = col >> 3, within = (col & 7) * 2;
-  uint4 out;
-  uint32_t* o = reinterpret_cast<uint32_t*>(&out);
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int kr = 16 * s + 8 * (g >> 1) + 4 * h + (i >> 2);
-    const char* p = tile + kr * 512 + ((chunk ^ (4 * (kr & 3))) << 4) + within;
-    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);  // generic -> LDS
-    const uint2 w = __builtin_bit_cast(uint2, v);
-    o[2 * h] = w.x;
-    o[2 * h + 1] = w.y;
-  }
-  return out;
+__device__ __forceinline__ uint32_t lds_addr_of(lds_char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
 // s_waitcnt with only vmcnt = n (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14,
@@ -417,19 +337,117 @@ __device__ __forceinline__ uint4 frag_mn(const char* tile, int c0, int s, int la
 #define TT_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8))
 
-template <int MODE, bool TRANS_B, int ET>
-__global__ __launch_bounds__(DM_NT) void gmm_dma_kernel(const char* __restrict__ p0,
-                                                        const char* __restrict__ p1,
-                                                        char* __restrict__ out, int64_t M,
-                                                        int64_t K, int64_t N, int E,
-                                                        const int64_t* __restrict__ counts,
-                                                        int tiles_i, int tiles_j) {
+// LDS operand tiles.
+// * K-major (k contiguous in memory): LDS row r (64 bytes = 32 k) holds tile
+//   row r, its 16-byte chunk c in slot c ^ ((r >> 2) & 3). An MFMA operand
+//   (32 rows, 8 k per lane) is one conflict-free ds_read_b128.
+// * MN-major (rows/columns contiguous in memory): LDS k-row kr (512 bytes)
+//   holds 256 columns, chunk c (columns 8c .. 8c + 7) in slot
+//   c ^ (4 * (kr & 3)). An operand is two gfx950 transposing reads
+//   (ds_read_b64_tr_b16): within each 16-lane group source lane i reads
+//   k-row k + i / 4, columns col + 4 * (i % 4) .. + 3, and lane i receives
+//   column col + i at the four k-rows. No register transpose is needed.
+// DMA: a wave fills 1 KiB per instruction, lane l at +16 l: K-major rows
+// 16u .. 16u + 15 (lane l -> row 16u + l / 4, slot l & 3); MN-major k-rows
+// 2u, 2u + 1 (lane l -> k-row 2u + l / 32, slot l & 31).
+
+// Fragment read offsets within an operand tile. K-major: rows r0 + lane % 32
+// at k-step s (further 32-row blocks add 2048 bytes).
+__device__ __forceinline__ uint32_t fragk_base(int r0, int s, int lane) {
+  const int r = r0 + (lane & 31);
+  const int c = 2 * s + (lane >> 5);
+  return (uint32_t)(r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
+}
+// MN-major: columns c0 .. c0 + 31; the second read is at +2048 and k-step s
+// adds 8192.
+__device__ __forceinline__ uint32_t fragmn_base(int c0, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int col = c0 + 16 * (g & 1) + 4 * (i & 3);
+  const int kr = 8 * (g >> 1) + (i >> 2);
+  return (uint32_t)(kr * 512 + (((col >> 3) ^ (4 * (kr & 3))) << 4) + (col & 7) * 2);
+}
+
+__device__ __forceinline__ uint4 read_k(lds_char* tile, uint32_t off) {
+  return __builtin_bit_cast(uint4, *reinterpret_cast<const lds_u32x4*>(tile + off));
+}
+__device__ __forceinline__ uint4 read_mn(lds_char* tile, uint32_t off) {
+  const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + off));
+  const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + off + 2048));
+  const uint2 w0 = __builtin_bit_cast(uint2, v0), w1 = __builtin_bit_cast(uint2, v1);
+  return uint4{w0.x, w0.y, w1.x, w1.y};
+}
+
+// Four fp32 values -> four 16-bit values (hardware round to nearest even).
+template <int ET>
+__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
+  if constexpr (ET == TT_BF16) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+    const bf16x2 lo = {(__bf16)a, (__bf16)b}, hi = {(__bf16)c, (__bf16)d};
+    return uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+  } else {
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+    const f16x2 lo = {(_Float16)a, (_Float16)b}, hi = {(_Float16)c, (_Float16)d};
+    return uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+  }
+}
+
+// Epilogue through LDS. The accumulators hold C^T blocks (the MFMA operands
+// are swapped): block (mi, ni) register 4g + e of lane l is
+// C[ri + 32 mi + l % 32][cj + 32 ni + 8 g + 4 (l / 32) + e]. Each wave writes
+// its 128x128 tile row-major into its own 32 KiB of LDS (16-byte chunks
+// XOR-swizzled by row), then stores four full 256-byte rows per instruction.
+// Column chunks never straddle the edge (J % 8 == 0).
+template <int ET>
+__device__ __forceinline__ void store_wave_tile(const f32x16 (&acc)[4][4], const TileDesc& t,
+                                                int64_t ri, int64_t cj, int lane,
+                                                lds_char* region) {
+  const int r_l = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = 32 * mi + r_l;
+        const int chunk = 4 * ni + g;
+        const uint2 v = pack4<ET>(acc[mi][ni][4 * g], acc[mi][ni][4 * g + 1],
+                                  acc[mi][ni][4 * g + 2], acc[mi][ni][4 * g + 3]);
+        *reinterpret_cast<lds_u32x2*>(region + r * 256 + ((chunk ^ (r & 15)) << 4) + 8 * h) =
+            u32x2{v.x, v.y};
+      }
+  const int c = lane & 15;
+  const int64_t gcol = cj + 8 * c;
+  const bool col_ok = gcol < t.J;
+#pragma unroll
+  for (int q = 0; q < 32; ++q) {
+    const int r = 4 * q + (lane >> 4);
+    const uint4 v = read_k(region, (uint32_t)(r * 256 + ((c ^ (r & 15)) << 4)));
+    const int64_t grow = ri + r;
+    if (col_ok && grow < t.I) *reinterpret_cast<uint4*>(t.c + (grow * t.ldc + gcol) * 2) = v;
+  }
+}
+
+// One block computes a 256x256 tile of one expert; wave w owns the 128x128
+// quarter (w / 2, w % 2). Operands stream through four LDS stages (32 KiB
+// each: A tile, B tile) with buffer loads straight into LDS; waves 0-1 load
+// A, waves 2-3 load B, 8 chunks of 16 bytes per lane per k-tile. Each buffer
+// resource covers exactly the operand (this expert's activation rows, or
+// this expert's weights), so rows past the expert's end and reduction rows
+// past its length read as zeros in hardware; column overhang inside the
+// operand only feeds output rows/columns that are never stored. The
+// reduction tail of a K-major operand whose length is not a multiple of 32
+// (KMASK) is masked explicitly.
+template <int MODE, bool TRANS_B, int ET, bool KMASK>
+__global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict__ p0,
+                                                         const char* __restrict__ p1,
+                                                         char* __restrict__ out, int64_t M,
+                                                         int64_t K, int64_t N, int E,
+                                                         const int64_t* __restrict__ counts,
+                                                         int tiles_i, int tiles_j) {
   typedef Layout<MODE, TRANS_B> Lay;
-  constexpr int WGN = 4, WTM = 128, WTN = 64, FM = WTM / 32, FN = WTN / 32;
+  constexpr int WT = 128, FM = 4, FN = 4;
   // One static LDS array per stage and a k-loop unrolled by the stage count:
-  // every DMA and every read then names a fixed array, so the compiler can
-  // tell that loads in flight to one stage do not alias reads of another and
-  // need not drain the DMA queue before reading.
+  // every address is then a compile-time stage base plus a lane offset.
   __shared__ __align__(16) char stage0[DM_STAGE];
   __shared__ __align__(16) char stage1[DM_STAGE];
   __shared__ __align__(16) char stage2[DM_STAGE];
@@ -444,23 +462,72 @@ __global__ __launch_bounds__(DM_NT) void gmm_dma_kernel(const char* __restrict__
                                                                  tile_start, t))
     return;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave / WGN, wn = wave % WGN;
-  const bool a_role = wave < 4;  // waves 0-3 stream A, waves 4-7 stream B
-  const int wv = wave & 3;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const bool a_role = wave < 2;
+  const int wv = wave & 1;
   const int nkt = (int)((t.R + DM_BK - 1) / DM_BK);
-  // A rows past the segment (fwd/dgrad) read as zeros.
-  const int64_t a_rows = Lay::A_K ? t.nrows : t.I;
 
-  DmaPlan plan;
-  if (a_role) {
-    plan = Lay::A_K ? plan_kmajor(t.a, t.lda, t.i0, a_rows, 0, wv, lane)
-                    : plan_mnmajor(t.a, t.lda, t.i0, t.I, 0, wv, lane);
+  // This wave's operand: buffer resource, per-chunk byte offsets at k-tile 0
+  // and the per-k-tile advance.
+  const char* obase = a_role ? t.a : t.b;
+  const int64_t ld = a_role ? t.lda : t.ldb;
+  const bool kmaj = a_role ? Lay::A_K : Lay::B_K;
+  const int64_t orow0 = a_role ? t.i0 : t.j0;
+  int64_t obytes;
+  if (a_role) obytes = (Lay::A_K ? t.nrows : t.R) * t.lda * 2;
+  else obytes = (MODE == MODE_WGRAD) ? t.R * t.ldb * 2 : K * N * 2;
+  const i32x4 rsrc = make_rsrc(obase, obytes);
+  uint32_t voff[8];
+  int kof[8];
+  uint32_t kstep;
+  if (kmaj) {
+    const int c = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t r = orow0 + 128 * wv + 16 * q + (lane >> 2);
+      voff[q] = (uint32_t)((r * ld + 8 * c) * 2);
+      kof[q] = 8 * c;
+    }
+    kstep = DM_BK * 2;
   } else {
-    plan = Lay::B_K ? plan_kmajor(t.b, t.ldb, t.j0, t.J, DM_TILE, wv, lane)
-                    : plan_mnmajor(t.b, t.ldb, t.j0, t.J, DM_TILE, wv, lane);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int kr = 2 * (wv * 8 + q) + (lane >> 5);
+      const int c = (lane & 31) ^ (4 * (kr & 3));
+      voff[q] = (uint32_t)((kr * ld + orow0 + 8 * c) * 2);
+      kof[q] = kr;
+    }
+    kstep = (uint32_t)(DM_BK * ld * 2);
   }
-  auto issue = [&](char* stg, int kt) { dma_issue(plan, stg, kt, t.R, wv); };
+  const uint32_t dst_wave = (a_role ? 0u : (uint32_t)DM_TILE) + (uint32_t)wv * 8192u;
+  const int kvalid = (int)t.R;
+
+  // Chunk q of k-tile kt into stage `stg`.
+  auto issue_one = [&](lds_char* stg, int kt, int q) {
+    uint32_t off = voff[q] + (uint32_t)kt * kstep;
+    if constexpr (KMASK) {
+      if (kmaj && kt * DM_BK + kof[q] >= kvalid) off = DM_OOB;
+    }
+    dma16(off, rsrc, lds_addr_of(stg) + dst_wave + (uint32_t)q * 1024u);
+  };
+  auto issue = [&](lds_char* stg, int kt) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) issue_one(stg, kt, q);
+  };
+
+  // Fragment read offsets (K-major: per k-step; MN-major: per 32-wide block).
+  uint32_t a_off[2], b_off[2], a_mn[FM], b_mn[FN];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    a_off[s] = fragk_base(wm * WT, s, lane);
+    b_off[s] = fragk_base(wn * WT, s, lane) + DM_TILE;
+  }
+#pragma unroll
+  for (int mi = 0; mi < FM; ++mi) a_mn[mi] = fragmn_base(wm * WT + mi * 32, lane);
+#pragma unroll
+  for (int ni = 0; ni < FN; ++ni) b_mn[ni] = fragmn_base(wn * WT + ni * 32, lane) + DM_TILE;
 
   f32x16 acc[FM][FN];
 #pragma unroll
@@ -470,59 +537,84 @@ __global__ __launch_bounds__(DM_NT) void gmm_dma_kernel(const char* __restrict__
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
 
-  // The operand reads of both k-steps of the tile are issued before its
-  // MFMAs, so the second step's LDS latency hides under the first step's
-  // MFMAs (the compiler alone loads each fragment just before its use).
-  constexpr int KS = DM_BK / 16;
-  static_assert(KS == 2, "two k-steps per tile");
-  auto load_frags = [&](const char* stg, int s, uint4 (&fa)[FM], uint4 (&fb)[FN]) {
+  // Current fragment offsets, re-materialised once per half step so that the
+  // compiler keeps one register per offset instead of one per stage.
+  uint32_t ao[2], bo[2], am[FM], bm[FN];
+  auto refresh = [&]() {
+    ao[0] = a_off[0]; ao[1] = a_off[1]; bo[0] = b_off[0]; bo[1] = b_off[1];
 #pragma unroll
-    for (int mi = 0; mi < FM; ++mi)
-      fa[mi] = Lay::A_K ? frag_k(stg, wm * WTM + mi * 32, s, lane)
-                        : frag_mn(stg, wm * WTM + mi * 32, s, lane);
+    for (int i = 0; i < FM; ++i) am[i] = a_mn[i];
 #pragma unroll
-    for (int ni = 0; ni < FN; ++ni)
-      fb[ni] = Lay::B_K ? frag_k(stg + DM_TILE, wn * WTN + ni * 32, s, lane)
-                        : frag_mn(stg + DM_TILE, wn * WTN + ni * 32, s, lane);
+    for (int i = 0; i < FN; ++i) bm[i] = b_mn[i];
+    if constexpr (Lay::A_K) asm volatile("" : "+v"(ao[0]), "+v"(ao[1]));
+    else asm volatile("" : "+v"(am[0]), "+v"(am[1]), "+v"(am[2]), "+v"(am[3]));
+    if constexpr (Lay::B_K) asm volatile("" : "+v"(bo[0]), "+v"(bo[1]));
+    else asm volatile("" : "+v"(bm[0]), "+v"(bm[1]), "+v"(bm[2]), "+v"(bm[3]));
   };
-  auto mfmas = [&](const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
-#pragma unroll
-    for (int mi = 0; mi < FM; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < FN; ++ni) acc[mi][ni] = Mma<ET>::run(fa[mi], fb[ni], acc[mi][ni]);
+  // Fragment unit i (0..FM-1: A block i, FM..: B block i - FM) of k-step s.
+  auto frag = [&](lds_char* stg, int s, int i, uint4 (&fa)[FM], uint4 (&fb)[FN]) {
+    if (i < FM)
+      fa[i] = Lay::A_K ? read_k(stg, ao[s] + i * 2048) : read_mn(stg, am[i] + s * 8192);
+    else
+      fb[i - FM] = Lay::B_K ? read_k(stg, bo[s] + (i - FM) * 2048)
+                            : read_mn(stg, bm[i - FM] + s * 8192);
   };
-  auto compute = [&](const char* stg) {
-    uint4 fa0[FM], fb0[FN], fa1[FM], fb1[FN];
-    load_frags(stg, 0, fa0, fb0);
-    load_frags(stg, 1, fa1, fb1);
-    mfmas(fa0, fb0);
-    mfmas(fa1, fb1);
+  // Operands swapped: the accumulator holds C^T blocks, so each lane owns one
+  // output row and four consecutive columns per register group.
+  auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
+    acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
   };
 
-  // Pipeline: tiles kt+1 .. kt+3 are in flight while tile kt is multiplied.
-  // Each wave waits for its own loads of tile kt (vmcnt), then the barrier
-  // makes every wave's loads visible and retires all reads of tile kt-1,
-  // whose stage then receives tile kt+3. One barrier per k-tile.
-  auto step = [&](int kt, char* cur, char* refill) {
-    const int last = (kt + DM_ST - 2 < nkt - 1) ? kt + DM_ST - 2 : nkt - 1;
-    const int ahead = last - kt;  // tiles issued after kt: 0, 1 or 2
-    if (ahead >= 2) TT_WAIT_VMCNT(8);
-    else if (ahead == 1) TT_WAIT_VMCNT(4);
-    else TT_WAIT_VMCNT(0);
+  lds_char* const s0 = (lds_char*)stage0;
+  lds_char* const s1 = (lds_char*)stage1;
+  lds_char* const s2 = (lds_char*)stage2;
+  lds_char* const s3 = (lds_char*)stage3;
+  uint4 a0[FM], b0[FN], a1[FM], b1[FN];
+  // Tile kt: multiply k-step 0 (a0/b0) while reading k-step 1; wait for tile
+  // kt+1 (tile kt+2 stays in flight), barrier (every wave is past its reads
+  // of tile kt-1); multiply k-step 1 while reading k-step 0 of tile kt+1 and
+  // refilling the stage of tile kt-1 with tile kt+3. One MFMA, one fragment
+  // read and one DMA chunk per slot, in this order (sched_barrier pins it).
+  // Loads past the last tile fall outside the resource (zeros) and land in
+  // stages that are never read again.
+  auto step = [&](int kt, lds_char* cur, lds_char* nxt, lds_char* refill) {
+    refresh();
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+      mfma(i, a0, b0);
+      if (i < FM + FN) frag(cur, 1, i, a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    TT_WAIT_VMCNT(8);
     __builtin_amdgcn_s_barrier();
-    if (kt + DM_ST - 1 < nkt) issue(refill, kt + DM_ST - 1);
-    compute(cur);
+    refresh();
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+      mfma(i, a1, b1);
+      if (i < FM + FN) frag(nxt, 0, i, a0, b0);
+      if (i < 8) issue_one(refill, kt + 3, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  if (nkt > 0) issue(stage0, 0);
-  if (nkt > 1) issue(stage1, 1);
-  if (nkt > 2) issue(stage2, 2);
+
+  issue(s0, 0);
+  issue(s1, 1);
+  issue(s2, 2);
+  TT_WAIT_VMCNT(16);
+  __builtin_amdgcn_s_barrier();
+  refresh();
+#pragma unroll
+  for (int i = 0; i < FM + FN; ++i) frag(s0, 0, i, a0, b0);
   for (int kt = 0; kt < nkt; kt += DM_ST) {
-    step(kt, stage0, stage3);
-    if (kt + 1 < nkt) step(kt + 1, stage1, stage0);
-    if (kt + 2 < nkt) step(kt + 2, stage2, stage1);
-    if (kt + 3 < nkt) step(kt + 3, stage3, stage2);
+    step(kt, s0, s1, s3);
+    if (kt + 1 < nkt) step(kt + 1, s1, s2, s0);
+    if (kt + 2 < nkt) step(kt + 2, s2, s3, s1);
+    if (kt + 3 < nkt) step(kt + 3, s3, s0, s2);
   }
-  store_tile<ET, FM, FN>(acc, t, t.i0 + wm * WTM, t.j0 + wn * WTN, lane);
+  TT_WAIT_VMCNT(0);  // every DMA has landed before the stages are reused
+  __syncthreads();   // every wave is past its last fragment read
+  lds_char* const region = wave == 0 ? s0 : wave == 1 ? s1 : wave == 2 ? s2 : s3;
+  store_wave_tile<ET>(acc, t, t.i0 + wm * WT, t.j0 + wn * WT, lane, region);
 }
 
 // ===========================================================================
@@ -855,23 +947,39 @@ int allow_lds(F* kernel, size_t lds, size_t& allowed) {
   return TT_OK;
 }
 
+template <int MODE, bool TB, int ET, bool KMASK>
+int launch_mfma_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
+                  int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj) {
+  const size_t lds = schedule_bytes(E);  // the stages are static LDS
+  static size_t allowed = 64 * 1024;
+  const int rc = allow_lds(&gmm_mfma_kernel<MODE, TB, ET, KMASK>, lds, allowed);
+  if (rc != TT_OK) return rc;
+  hipLaunchKernelGGL((gmm_mfma_kernel<MODE, TB, ET, KMASK>), dim3((unsigned)nblk), dim3(DM_NT),
+                     lds, s, static_cast<const char*>(p0), static_cast<const char*>(p1),
+                     static_cast<char*>(out), M, K, N, E, counts, ti, tj);
+  return tt_check_launch("gmm");
+}
+
 template <int MODE, bool TB, int ET>
-int launch_dma(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N, int E,
-               const int64_t* counts, hipStream_t s) {
+int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
+                int E, const int64_t* counts, hipStream_t s) {
   int ti, tj;
   const int64_t nblk = grid_blocks(MODE, TB, M, K, N, E, DM_BM, DM_BN, ti, tj);
   if (nblk == 0) return TT_OK;
   TT_REQUIRE(nblk < 0x7fffffff, "gmm: grid too large");
-  const size_t lds = schedule_bytes(E);  // the stages are static LDS
-  TT_REQUIRE(lds + (size_t)DM_ST * DM_STAGE <= 160 * 1024,
+  TT_REQUIRE(schedule_bytes(E) + (size_t)DM_ST * DM_STAGE <= 160 * 1024,
              "gmm: too many experts for the LDS tile schedule");
-  static size_t allowed = 64 * 1024;
-  const int rc = allow_lds(&gmm_dma_kernel<MODE, TB, ET>, lds, allowed);
-  if (rc != TT_OK) return rc;
-  hipLaunchKernelGGL((gmm_dma_kernel<MODE, TB, ET>), dim3((unsigned)nblk), dim3(DM_NT), lds, s,
-                     static_cast<const char*>(p0), static_cast<const char*>(p1),
-                     static_cast<char*>(out), M, K, N, E, counts, ti, tj);
-  return tt_check_launch("gmm");
+  // Operands are addressed through 32-bit buffer offsets: every activation
+  // matrix (plus a tile of overhang) and every expert weight must stay below
+  // 4 GiB.
+  const int64_t ld = K > N ? K : N;
+  TT_REQUIRE((M + DM_BM) * ld * 2 < (int64_t)DM_OOB && K * N * 2 < (int64_t)DM_OOB,
+             "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
+             (long long)M, (long long)K, (long long)N);
+  const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length of fwd / dgrad
+  if (MODE != MODE_WGRAD && R % DM_BK)
+    return launch_mfma_k<MODE, TB, ET, true>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
+  return launch_mfma_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
 }
 
 template <int MODE, bool TB, bool FP8, int ET>
@@ -924,11 +1032,11 @@ int dispatch(const void* p0, const void* p1, int dtype, int64_t m, int64_t k, in
                reinterpret_cast<uintptr_t>(out)) & 15) == 0,
              "gmm: operands must be 16-byte aligned");
   if (dtype == TT_BF16) {
-    if (tb) return launch_dma<MODE, true, TT_BF16>(p0, p1, out, m, k, n, E, counts, s);
-    return launch_dma<MODE, false, TT_BF16>(p0, p1, out, m, k, n, E, counts, s);
+    if (tb) return launch_mfma<MODE, true, TT_BF16>(p0, p1, out, m, k, n, E, counts, s);
+    return launch_mfma<MODE, false, TT_BF16>(p0, p1, out, m, k, n, E, counts, s);
   }
-  if (tb) return launch_dma<MODE, true, TT_F16>(p0, p1, out, m, k, n, E, counts, s);
-  return launch_dma<MODE, false, TT_F16>(p0, p1, out, m, k, n, E, counts, s);
+  if (tb) return launch_mfma<MODE, true, TT_F16>(p0, p1, out, m, k, n, E, counts, s);
+  return launch_mfma<MODE, false, TT_F16>(p0, p1, out, m, k, n, E, counts, s);
 }
 
 }  // namespace
