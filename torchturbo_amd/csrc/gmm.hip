@@ -196,15 +196,31 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
     it = rem / tiles_j;
     jt = rem % tiles_j;
     if (rank >= E) return false;
+    // Rank of every expert, its comparisons split over NT / E threads per
+    // expert and summed with LDS atomics; int32 counts after the schedule.
+    int* cnt = tile_start + E + 1;
+    int* rnk = cnt + E;
     for (int x = threadIdx.x; x < E; x += NT) {
-      const int64_t cx = row_start[x + 1] - row_start[x];
-      int r = 0;
-      for (int y = 0; y < E; ++y) {
-        const int64_t cy = row_start[y + 1] - row_start[y];
-        r += (cy > cx) || (cy == cx && y < x);
-      }
-      if (r == rank) lpt_expert = x;
+      cnt[x] = (int)(row_start[x + 1] - row_start[x]);
+      rnk[x] = 0;
     }
+    __syncthreads();
+    const int parts = E >= NT ? 1 : NT / E;
+    for (int idx = threadIdx.x; idx < E * parts; idx += NT) {
+      const int x = idx % E, part = idx / E;
+      const int y0 = part * E / parts, y1 = (part + 1) * E / parts;
+      const int cx = cnt[x];
+      int r = 0;
+#pragma unroll 8
+      for (int y = y0; y < y1; ++y) {
+        const int cy = cnt[y];
+        r += (cy > cx) | ((cy == cx) & (y < x));
+      }
+      atomicAdd(&rnk[x], r);
+    }
+    __syncthreads();
+    for (int x = threadIdx.x; x < E; x += NT)
+      if (rnk[x] == rank) lpt_expert = x;
     __syncthreads();
     e = lpt_expert;
   } else {
@@ -912,7 +928,11 @@ __global__ __launch_bounds__(256) void gmm_f32_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-size_t schedule_bytes(int E) { return (size_t)(E + 1) * (sizeof(int64_t) + sizeof(int)) + 64; }
+// Expert schedule in dynamic LDS: row starts (int64), m-tile starts (int),
+// and for the weight-gradient ranking int32 counts and ranks.
+size_t schedule_bytes(int E) {
+  return (size_t)(E + 1) * (sizeof(int64_t) + sizeof(int)) + (size_t)E * 2 * sizeof(int) + 64;
+}
 
 // Grid of a grouped launch: fwd/dgrad use an upper bound on the number of
 // (m-tile, n-tile) slots (each expert adds at most one partial m-tile);

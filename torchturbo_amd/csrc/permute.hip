@@ -117,6 +117,91 @@ __global__ __launch_bounds__(256) void unpermute_gather_kernel(
   }
 }
 
+// Same sum for top-k <= KMAX (small): every thread reads the token's row ids
+// (uniform loads), sorts them in registers, issues all K row loads before
+// adding, and accumulates in ascending row order. No block barrier, no LDS.
+// Row ids outside [0, M) contribute nothing (adding +0 to a sum that starts
+// at +0 leaves it unchanged, so skipping and adding zero agree bitwise).
+template <int DT>
+__device__ __forceinline__ float rnd_dt(float v) {
+  if constexpr (DT == TT_BF16) return bf16_to_f32(f32_to_bf16(v));
+  else if constexpr (DT == TT_F16) return f16_to_f32(f32_to_f16(v));
+  else return v;
+}
+template <int PD>
+__device__ __forceinline__ float load_w(const void* p, int64_t i) {
+  if constexpr (PD == TT_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (PD == TT_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+constexpr int kNoProbs = -1;
+
+template <class TT, int XD, int PD, int V, int KMAX>
+__global__ __launch_bounds__(256) void unpermute_small_kernel(
+    const typename TT::storage* __restrict__ packed, int64_t H, int K,
+    const int32_t* __restrict__ rows, const int64_t* __restrict__ experts,
+    const void* __restrict__ probs, int E, typename TT::storage* __restrict__ out, int64_t M) {
+  typedef typename TT::storage St;
+  constexpr int PR = (PD == kNoProbs || PD == XD) ? XD : TT_F32;
+  const int64_t t = blockIdx.x;
+  int rs[KMAX];
+  float ws[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    rs[j] = 0x7fffffff;
+    ws[j] = 1.0f;
+    if (j < K) {
+      const int r = rows[t * K + j];
+      rs[j] = (r >= 0 && r < M) ? r : 0x7fffffff;
+      if constexpr (PD != kNoProbs) {
+        const int64_t e = experts[t * K + j];
+        ws[j] = (e >= 0 && e < E) ? load_w<PD>(probs, t * E + e) : 1.0f;
+      }
+    }
+  }
+  // Insertion sort by row (K <= KMAX <= 8), carrying the weights.
+#pragma unroll
+  for (int a = 1; a < KMAX; ++a)
+#pragma unroll
+    for (int b = a; b > 0; --b) {
+      const bool sw = rs[b - 1] > rs[b];
+      const int r0 = rs[b - 1], r1 = rs[b];
+      const float w0 = ws[b - 1], w1 = ws[b];
+      rs[b - 1] = sw ? r1 : r0;
+      rs[b] = sw ? r0 : r1;
+      ws[b - 1] = sw ? w1 : w0;
+      ws[b] = sw ? w0 : w1;
+    }
+  const int64_t nv = H / V;
+  for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
+    St x[KMAX][V];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (rs[j] != 0x7fffffff) {
+        __builtin_memcpy(x[j], packed + (int64_t)rs[j] * H + v * V, sizeof(x[j]));
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) x[j][i] = TT::from_f32(0.0f);
+      }
+    }
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        if constexpr (PD != kNoProbs) acc[i] += rnd_dt<PR>(TT::to_f32(x[j][i]) * ws[j]);
+        else acc[i] += TT::to_f32(x[j][i]);
+      }
+    St y[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) y[i] = TT::from_f32(rnd_dt<PR>(acc[i]));
+    __builtin_memcpy(out + t * H + v * V, y, sizeof(y));
+  }
+}
+
 // Weighted-unpermute backward. grad_packed[r_j] = cast(grad_out[t] * w_j);
 // grad_probs[t, e_j] = sum_h grad_out[t, h] * packed[r_j, h]; zeros elsewhere.
 template <class TT, int V, int KMAX>
@@ -273,7 +358,7 @@ unsigned block_for(int64_t nv) {
 
 bool float_dtype(int d) { return d == TT_F32 || d == TT_BF16 || d == TT_F16; }
 
-template <class TT>
+template <class TT, int XD>
 int launch_unpermute(const void* packed, int64_t T, int64_t H, int K, const int32_t* rows,
                      const int64_t* experts, const void* probs, int pdt, int E, int prod_dt,
                      void* out, int64_t M, hipStream_t s) {
@@ -283,7 +368,25 @@ int launch_unpermute(const void* packed, int64_t T, int64_t H, int K, const int3
                        static_cast<uintptr_t>(H * esz);
   const St* p = static_cast<const St*>(packed);
   St* o = static_cast<St*>(out);
-  if (al % 16 == 0) {
+  if (al % 16 == 0 && K <= 8) {
+    constexpr int V = 16 / sizeof(St);
+    const dim3 grid((unsigned)T), blk(block_for(H / V));
+    if (probs == nullptr) {
+      if (K <= 2)
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      else
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+    } else if (pdt == TT_F32) {
+      if (K <= 2)
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      else
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+    } else if (pdt == TT_BF16) {
+      hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_BF16, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+    } else {
+      hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F16, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+    }
+  } else if (al % 16 == 0) {
     constexpr int V = 16 / sizeof(St);
     hipLaunchKernelGGL((unpermute_gather_kernel<TT, V>), dim3(T), dim3(block_for(H / V)), 0, s, p,
                        H, K, rows, experts, probs, pdt, E, prod_dt, o, M);
@@ -373,9 +476,9 @@ extern "C" int tt_unpermute_gather(const void* packed, int dtype, int64_t num_to
   const int64_t M = num_tokens * topk;
   hipStream_t s = S(stream);
   switch (dtype) {
-    case TT_BF16: return launch_unpermute<BF16T>(packed, num_tokens, hidden, topk, row_indices, expert_indices, probs, probs_dtype, num_experts, prod_dt, out, M, s);
-    case TT_F16: return launch_unpermute<F16T>(packed, num_tokens, hidden, topk, row_indices, expert_indices, probs, probs_dtype, num_experts, prod_dt, out, M, s);
-    default: return launch_unpermute<F32T>(packed, num_tokens, hidden, topk, row_indices, expert_indices, probs, probs_dtype, num_experts, prod_dt, out, M, s);
+    case TT_BF16: return launch_unpermute<BF16T, TT_BF16>(packed, num_tokens, hidden, topk, row_indices, expert_indices, probs, probs_dtype, num_experts, prod_dt, out, M, s);
+    case TT_F16: return launch_unpermute<F16T, TT_F16>(packed, num_tokens, hidden, topk, row_indices, expert_indices, probs, probs_dtype, num_experts, prod_dt, out, M, s);
+    default: return launch_unpermute<F32T, TT_F32>(packed, num_tokens, hidden, topk, row_indices, expert_indices, probs, probs_dtype, num_experts, prod_dt, out, M, s);
   }
 }
 

@@ -8,8 +8,14 @@
 //   g  = grad_out (as fp32);         da = round_x(g * p)
 //   dp = sum_f g * a  (per row)      ds = round(da * up);  dup = round(da * s)
 //   dgate = round(ds * sigmoid(gate) * (1 + gate * (1 - sigmoid(gate))))
-// Elementwise passes are HBM-bound; rows are handled by one wave each so the
-// per-row probability gradient is a wave reduction.
+//
+// Layout: a row is handled by L lanes (a power of two chosen so that the
+// row's 16-byte vectors divide evenly), 64 / L rows per wave; the per-row
+// probability gradient is a reduction over those L lanes. All dtype choices
+// are template parameters, so the element loop is branch-free. For 16-bit
+// data the sigmoid uses the hardware exp2 and reciprocal (a few ulp in fp32,
+// far below the 16-bit rounding that follows); fp32 data keeps expf and a
+// correctly rounded division.
 #include <math.h>
 
 #include "common.h"
@@ -18,87 +24,153 @@ namespace {
 
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+constexpr int NO_PROBS = -1;
 
-template <class TT, int V>
-__global__ __launch_bounds__(256) void swiglu_fwd_kernel(
-    const typename TT::storage* __restrict__ x, int64_t rows, int64_t F,
-    const void* __restrict__ probs, int pdt, int prod_dt, int xdt,
-    typename TT::storage* __restrict__ out) {
-  typedef typename TT::storage St;
-  const int64_t nv = F / V;
-  const int64_t total = rows * nv;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / nv;
-    const int64_t v = i - r * nv;
-    St g[V], u[V], o[V];
-    __builtin_memcpy(g, x + r * 2 * F + v * V, sizeof(g));
-    __builtin_memcpy(u, x + r * 2 * F + F + v * V, sizeof(u));
-    const float p = probs != nullptr ? load_as_f32(probs, pdt, r) : 1.0f;
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-      const float s = round_to(silu_f(TT::to_f32(g[k])), xdt);
-      float a = round_to(s * TT::to_f32(u[k]), xdt);
-      if (probs != nullptr) a = round_to(a * p, prod_dt);
-      o[k] = TT::from_f32(a);
-    }
-    __builtin_memcpy(out + r * F + v * V, o, sizeof(o));
+template <class TT>
+struct Traits;
+template <>
+struct Traits<BF16T> { static constexpr int code = TT_BF16; };
+template <>
+struct Traits<F16T> { static constexpr int code = TT_F16; };
+template <>
+struct Traits<F32T> { static constexpr int code = TT_F32; };
+
+template <int DT>
+__device__ __forceinline__ float rnd(float v) {
+  if constexpr (DT == TT_BF16) return bf16_to_f32(f32_to_bf16(v));
+  else if constexpr (DT == TT_F16) return f16_to_f32(f32_to_f16(v));
+  else return v;
+}
+
+template <int PD>
+__device__ __forceinline__ float load_prob(const void* p, int64_t r) {
+  if constexpr (PD == TT_F32) return static_cast<const float*>(p)[r];
+  else if constexpr (PD == TT_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[r]);
+  else if constexpr (PD == TT_F16) return f16_to_f32(static_cast<const uint16_t*>(p)[r]);
+  else return 1.0f;
+}
+
+template <int PD>
+__device__ __forceinline__ void store_prob(void* p, int64_t r, float v) {
+  if constexpr (PD == TT_F32) static_cast<float*>(p)[r] = v;
+  else if constexpr (PD == TT_BF16) static_cast<uint16_t*>(p)[r] = f32_to_bf16(v);
+  else if constexpr (PD == TT_F16) static_cast<uint16_t*>(p)[r] = f32_to_f16(v);
+}
+
+// sigmoid(g) and silu(g) = g / (1 + exp(-g)).
+template <class TT>
+__device__ __forceinline__ void sig_silu(float g, float& sig, float& silu) {
+  if constexpr (Traits<TT>::code == TT_F32) {
+    const float den = 1.0f + expf(-g);
+    sig = 1.0f / den;
+    silu = g / den;
+  } else {
+    sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+    silu = g * sig;
   }
 }
 
-template <class TT, int V>
+constexpr int promote(int a, int b) { return (b == NO_PROBS || a == b) ? a : TT_F32; }
+
+template <class TT, int PD, int V>
+__global__ __launch_bounds__(256) void swiglu_fwd_kernel(const typename TT::storage* __restrict__ x,
+                                                         int64_t rows, int64_t F,
+                                                         const void* __restrict__ probs, int L,
+                                                         typename TT::storage* __restrict__ out) {
+  typedef typename TT::storage St;
+  constexpr int XD = Traits<TT>::code, PR = promote(XD, PD);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
+  if (r >= rows) return;
+  const float p = load_prob<PD>(probs, r);
+  const St* xr = x + r * 2 * F;
+  St* orow = out + r * F;
+  const int64_t nv = F / V;
+  for (int64_t v = lane & (L - 1); v < nv; v += L) {
+    St g[V], u[V], o[V];
+    __builtin_memcpy(g, xr + v * V, sizeof(g));
+    __builtin_memcpy(u, xr + F + v * V, sizeof(u));
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      float sig, si;
+      sig_silu<TT>(TT::to_f32(g[k]), sig, si);
+      float a = rnd<XD>(rnd<XD>(si) * TT::to_f32(u[k]));
+      if constexpr (PD != NO_PROBS) a = rnd<PR>(a * p);
+      o[k] = TT::from_f32(a);
+    }
+    __builtin_memcpy(orow + v * V, o, sizeof(o));
+  }
+}
+
+template <class TT, int PD, int V, bool GP>
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     const typename TT::storage* __restrict__ x, int64_t rows, int64_t F,
-    const void* __restrict__ probs, int pdt, int prod_dt, int xdt,
-    const typename TT::storage* __restrict__ gout, typename TT::storage* __restrict__ gx,
-    void* __restrict__ gprobs) {
+    const void* __restrict__ probs, int L, const typename TT::storage* __restrict__ gout,
+    typename TT::storage* __restrict__ gx, void* __restrict__ gprobs) {
   typedef typename TT::storage St;
-  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / TT_WAVE) + (threadIdx.x >> 6);
-  if (r >= rows) return;  // whole wave
-  const int lane = lane_id();
-  const float p = probs != nullptr ? load_as_f32(probs, pdt, r) : 1.0f;
+  constexpr int XD = Traits<TT>::code, PR = promote(XD, PD);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
+  const bool live = r < rows;  // idle lanes still join the row reduction
+  const float p = live ? load_prob<PD>(probs, r) : 0.f;
   float dp = 0.f;
-  const int64_t nv = F / V;
-  for (int64_t v = lane; v < nv; v += TT_WAVE) {
+  const int64_t nv = live ? F / V : 0;
+  const St* xr = x + r * 2 * F;
+  const St* gr = gout + r * F;
+  St* dxr = gx + r * 2 * F;
+  for (int64_t v = lane & (L - 1); v < nv; v += L) {
     St g[V], u[V], d[V], og[V], ou[V];
-    __builtin_memcpy(g, x + r * 2 * F + v * V, sizeof(g));
-    __builtin_memcpy(u, x + r * 2 * F + F + v * V, sizeof(u));
-    __builtin_memcpy(d, gout + r * F + v * V, sizeof(d));
+    __builtin_memcpy(g, xr + v * V, sizeof(g));
+    __builtin_memcpy(u, xr + F + v * V, sizeof(u));
+    __builtin_memcpy(d, gr + v * V, sizeof(d));
 #pragma unroll
     for (int k = 0; k < V; ++k) {
       const float gf = TT::to_f32(g[k]);
       const float uf = TT::to_f32(u[k]);
-      const float den = 1.0f + expf(-gf);
-      const float sig = 1.0f / den;
-      const float s = round_to(gf / den, xdt);
+      float sig, si;
+      sig_silu<TT>(gf, sig, si);
+      const float s = rnd<XD>(si);
       float da;
-      if (probs != nullptr) {
+      if constexpr (PD != NO_PROBS) {
         const float gd = TT::to_f32(d[k]);
-        const float a = round_to(s * uf, xdt);
-        dp += round_to(gd * a, prod_dt);
-        da = round_to(gd * p, xdt);
+        if constexpr (GP) dp += rnd<PR>(gd * rnd<XD>(s * uf));
+        da = rnd<XD>(gd * p);
       } else {
         da = TT::to_f32(d[k]);
       }
-      const float ds = round_to(da * uf, xdt);
+      const float ds = rnd<XD>(da * uf);
       ou[k] = TT::from_f32(da * s);
       og[k] = TT::from_f32(ds * (sig * (1.0f + gf * (1.0f - sig))));
     }
-    __builtin_memcpy(gx + r * 2 * F + v * V, og, sizeof(og));
-    __builtin_memcpy(gx + r * 2 * F + F + v * V, ou, sizeof(ou));
+    __builtin_memcpy(dxr + v * V, og, sizeof(og));
+    __builtin_memcpy(dxr + F + v * V, ou, sizeof(ou));
   }
-  if (gprobs != nullptr) {
-    dp = wave_sum(dp);
-    if (lane == 0) store_from_f32(gprobs, pdt, r, dp);
+  if constexpr (GP) {
+    for (int off = L / 2; off > 0; off >>= 1) dp += __shfl_xor(dp, off, TT_WAVE);
+    if (live && (lane & (L - 1)) == 0) store_prob<PD>(gprobs, r, dp);
   }
 }
 
 bool float_dtype(int d) { return d == TT_F32 || d == TT_BF16 || d == TT_F16; }
 
-template <class TT>
-int launch_fwd(const void* x, int64_t rows, int64_t F, const void* probs, int pdt, int prod_dt,
-               int xdt, void* out, hipStream_t s) {
+// Lanes per row: the power of two <= 64 that wastes the fewest lane slots
+// over the row's vectors (larger on ties).
+int lanes_per_row(int64_t nv) {
+  int best = 1;
+  int64_t best_waste = -1;
+  for (int L = 64; L >= 1; L >>= 1) {
+    const int64_t waste = ((nv + L - 1) / L) * L - nv;
+    if (best_waste < 0 || waste < best_waste) {
+      best = L;
+      best_waste = waste;
+    }
+  }
+  return best;
+}
+
+template <class TT, int PD>
+int launch_fwd_p(const void* x, int64_t rows, int64_t F, const void* probs, void* out,
+                 hipStream_t s) {
   typedef typename TT::storage St;
   const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
                        static_cast<uintptr_t>(F * sizeof(St));
@@ -106,37 +178,73 @@ int launch_fwd(const void* x, int64_t rows, int64_t F, const void* probs, int pd
   St* op = static_cast<St*>(out);
   if (al % 16 == 0) {
     constexpr int V = 16 / sizeof(St);
-    const int64_t total = rows * (F / V);
-    const unsigned grid = (unsigned)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
-    hipLaunchKernelGGL((swiglu_fwd_kernel<TT, V>), dim3(grid), dim3(256), 0, s, xp, rows, F,
-                       probs, pdt, prod_dt, xdt, op);
+    const int L = lanes_per_row(F / V);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, V>), dim3((unsigned)((rows + rpb - 1) / rpb)),
+                       dim3(256), 0, s, xp, rows, F, probs, L, op);
   } else {
-    const int64_t total = rows * F;
-    const unsigned grid = (unsigned)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
-    hipLaunchKernelGGL((swiglu_fwd_kernel<TT, 1>), dim3(grid), dim3(256), 0, s, xp, rows, F,
-                       probs, pdt, prod_dt, xdt, op);
+    const int L = lanes_per_row(F);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, 1>), dim3((unsigned)((rows + rpb - 1) / rpb)),
+                       dim3(256), 0, s, xp, rows, F, probs, L, op);
   }
   return tt_check_launch("swiglu_fwd");
 }
 
-template <class TT>
-int launch_bwd(const void* x, int64_t rows, int64_t F, const void* probs, int pdt, int prod_dt,
-               int xdt, const void* gout, void* gx, void* gprobs, hipStream_t s) {
+template <class TT, int PD, bool GP>
+int launch_bwd_p(const void* x, int64_t rows, int64_t F, const void* probs, const void* gout,
+                 void* gx, void* gprobs, hipStream_t s) {
   typedef typename TT::storage St;
   const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gout) |
                        reinterpret_cast<uintptr_t>(gx) | static_cast<uintptr_t>(F * sizeof(St));
-  const dim3 grid((unsigned)((rows + 3) / 4));
+  const St* xp = static_cast<const St*>(x);
+  const St* gp = static_cast<const St*>(gout);
+  St* dxp = static_cast<St*>(gx);
   if (al % 16 == 0) {
     constexpr int V = 16 / sizeof(St);
-    hipLaunchKernelGGL((swiglu_bwd_kernel<TT, V>), grid, dim3(256), 0, s, static_cast<const St*>(x),
-                       rows, F, probs, pdt, prod_dt, xdt, static_cast<const St*>(gout),
-                       static_cast<St*>(gx), gprobs);
+    const int L = lanes_per_row(F / V);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((swiglu_bwd_kernel<TT, PD, V, GP>),
+                       dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, xp, rows, F,
+                       probs, L, gp, dxp, gprobs);
   } else {
-    hipLaunchKernelGGL((swiglu_bwd_kernel<TT, 1>), grid, dim3(256), 0, s, static_cast<const St*>(x),
-                       rows, F, probs, pdt, prod_dt, xdt, static_cast<const St*>(gout),
-                       static_cast<St*>(gx), gprobs);
+    const int L = lanes_per_row(F);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((swiglu_bwd_kernel<TT, PD, 1, GP>),
+                       dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, xp, rows, F,
+                       probs, L, gp, dxp, gprobs);
   }
   return tt_check_launch("swiglu_bwd");
+}
+
+template <class TT>
+int launch_fwd(const void* x, int64_t rows, int64_t F, const void* probs, int pdt, void* out,
+               hipStream_t s) {
+  if (probs == nullptr) return launch_fwd_p<TT, NO_PROBS>(x, rows, F, probs, out, s);
+  switch (pdt) {
+    case TT_F32: return launch_fwd_p<TT, TT_F32>(x, rows, F, probs, out, s);
+    case TT_BF16: return launch_fwd_p<TT, TT_BF16>(x, rows, F, probs, out, s);
+    default: return launch_fwd_p<TT, TT_F16>(x, rows, F, probs, out, s);
+  }
+}
+
+template <class TT, int PD>
+int launch_bwd_g(const void* x, int64_t rows, int64_t F, const void* probs, const void* gout,
+                 void* gx, void* gprobs, hipStream_t s) {
+  if (gprobs != nullptr) return launch_bwd_p<TT, PD, true>(x, rows, F, probs, gout, gx, gprobs, s);
+  return launch_bwd_p<TT, PD, false>(x, rows, F, probs, gout, gx, gprobs, s);
+}
+
+template <class TT>
+int launch_bwd(const void* x, int64_t rows, int64_t F, const void* probs, int pdt,
+               const void* gout, void* gx, void* gprobs, hipStream_t s) {
+  if (probs == nullptr)
+    return launch_bwd_p<TT, NO_PROBS, false>(x, rows, F, probs, gout, gx, gprobs, s);
+  switch (pdt) {
+    case TT_F32: return launch_bwd_g<TT, TT_F32>(x, rows, F, probs, gout, gx, gprobs, s);
+    case TT_BF16: return launch_bwd_g<TT, TT_BF16>(x, rows, F, probs, gout, gx, gprobs, s);
+    default: return launch_bwd_g<TT, TT_F16>(x, rows, F, probs, gout, gx, gprobs, s);
+  }
 }
 
 }  // namespace
@@ -147,12 +255,11 @@ extern "C" int tt_swiglu_fwd(const void* x, int dtype, int64_t rows, int64_t ffn
   TT_REQUIRE(rows >= 0 && ffn >= 0, "swiglu: negative sizes");
   if (probs != nullptr) TT_REQUIRE(float_dtype(probs_dtype), "swiglu: unsupported probs dtype");
   if (rows == 0 || ffn == 0) return TT_OK;
-  const int prod_dt = probs != nullptr ? tt_promote(dtype, probs_dtype) : dtype;
   hipStream_t s = S(stream);
   switch (dtype) {
-    case TT_BF16: return launch_fwd<BF16T>(x, rows, ffn, probs, probs_dtype, prod_dt, dtype, out, s);
-    case TT_F16: return launch_fwd<F16T>(x, rows, ffn, probs, probs_dtype, prod_dt, dtype, out, s);
-    default: return launch_fwd<F32T>(x, rows, ffn, probs, probs_dtype, prod_dt, dtype, out, s);
+    case TT_BF16: return launch_fwd<BF16T>(x, rows, ffn, probs, probs_dtype, out, s);
+    case TT_F16: return launch_fwd<F16T>(x, rows, ffn, probs, probs_dtype, out, s);
+    default: return launch_fwd<F32T>(x, rows, ffn, probs, probs_dtype, out, s);
   }
 }
 
@@ -164,11 +271,10 @@ extern "C" int tt_swiglu_bwd(const void* x, int dtype, int64_t rows, int64_t ffn
   if (probs != nullptr) TT_REQUIRE(float_dtype(probs_dtype), "swiglu_bwd: unsupported probs dtype");
   if (grad_probs != nullptr) TT_REQUIRE(probs != nullptr, "swiglu_bwd: grad_probs needs probs");
   if (rows == 0) return TT_OK;
-  const int prod_dt = probs != nullptr ? tt_promote(dtype, probs_dtype) : dtype;
   hipStream_t s = S(stream);
   switch (dtype) {
-    case TT_BF16: return launch_bwd<BF16T>(x, rows, ffn, probs, probs_dtype, prod_dt, dtype, grad_out, grad_x, grad_probs, s);
-    case TT_F16: return launch_bwd<F16T>(x, rows, ffn, probs, probs_dtype, prod_dt, dtype, grad_out, grad_x, grad_probs, s);
-    default: return launch_bwd<F32T>(x, rows, ffn, probs, probs_dtype, prod_dt, dtype, grad_out, grad_x, grad_probs, s);
+    case TT_BF16: return launch_bwd<BF16T>(x, rows, ffn, probs, probs_dtype, grad_out, grad_x, grad_probs, s);
+    case TT_F16: return launch_bwd<F16T>(x, rows, ffn, probs, probs_dtype, grad_out, grad_x, grad_probs, s);
+    default: return launch_bwd<F32T>(x, rows, ffn, probs, probs_dtype, grad_out, grad_x, grad_probs, s);
   }
 }
