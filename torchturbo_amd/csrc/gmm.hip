@@ -8,7 +8,7 @@
 // K-major (k contiguous) or MN-major (i or j contiguous). v_mfma_f32_32x32x16
 // takes, per lane, 8 consecutive k of one row (A) or one column (B).
 //
-// Two kernels share the tile schedule:
+// The kernels share the tile schedule:
 //
 // * gmm_mfma_kernel (bf16/f16): 256x256x32 block tiles, 4 waves of 128x128
 //   (one wave per SIMD, 256 accumulator registers). Operands stream into
@@ -22,10 +22,12 @@
 //   MFMAs, fragment reads of the next k-step and DMA issue are interleaved
 //   one per slot. The epilogue converts to 16 bits in hardware and stores
 //   through LDS as full 256-byte rows.
-// * gmm_reg_kernel: 256x256x64 tiles through registers and two LDS stages,
-//   8x8 register transposes for MN-major operands. Used for FP8 weights: the
-//   e4m3 bytes are decoded and multiplied by their 128x128 block scale while
-//   staging, giving exactly bf16(f32(q) * f32(scale)).
+// * gmm_fp8_kernel (fwd/dgrad with e4m3 weights and 128x128 block scales):
+//   the same tiles and pipeline; the weight tile arrives in LDS as e4m3
+//   bytes and each wave decodes its own rows in hardware, multiplies by the
+//   block scale and rounds to bf16 (exactly bf16(f32(q) * f32(scale))) into
+//   one of three rotating bf16 tiles, overlapped with the previous k-tile's
+//   MFMAs. An fp32 fallback kernel serves fp32 operands.
 //
 // Tile schedule: fwd/dgrad blocks walk (expert, m-tile, n-tile) slots whose
 // count is only known on the device; every block derives its slot from the
@@ -55,7 +57,6 @@ struct Mma<TT_BF16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint16_t out(float f) { return f32_to_bf16(f); }
 };
 template <>
 struct Mma<TT_F16> {
@@ -63,42 +64,7 @@ struct Mma<TT_F16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint16_t out(float f) { return f32_to_f16(f); }
 };
-
-// 8x8 transpose of 16-bit elements: in[r] holds row r (8 elements), out[c]
-// holds column c.
-__device__ __forceinline__ void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
-  const uint32_t* s = reinterpret_cast<const uint32_t*>(in);
-  uint32_t* d = reinterpret_cast<uint32_t*>(out);
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const int w = c >> 1;  // source dword within each row
-    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      d[c * 4 + q] = __builtin_amdgcn_perm(s[(2 * q + 1) * 4 + w], s[(2 * q) * 4 + w], sel);
-  }
-}
-
-// One e4m3fn byte -> fp32 (exact). Via the f16 bit pattern: e4m3 shares the
-// 3-bit mantissa and its exponent bias differs by 8, so (byte & 0x7f) << 7
-// reinterpreted as f16 equals |value| * 2^-8, subnormals included.
-__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
-  const uint16_t h = static_cast<uint16_t>(((b & 0x80u) << 8) | ((b & 0x7fu) << 7));
-  const float v = f16_to_f32(h) * 256.0f;
-  return ((b & 0x7fu) == 0x7fu) ? __builtin_nanf("") : v;
-}
-
-// Four e4m3 bytes of `w` times `scale`, rounded to bf16, packed in two dwords.
-__device__ __forceinline__ uint2 dequant4(uint32_t w, float scale) {
-  uint2 r;
-  r.x = static_cast<uint32_t>(f32_to_bf16(e4m3_to_f32(w & 0xffu) * scale)) |
-        (static_cast<uint32_t>(f32_to_bf16(e4m3_to_f32((w >> 8) & 0xffu) * scale)) << 16);
-  r.y = static_cast<uint32_t>(f32_to_bf16(e4m3_to_f32((w >> 16) & 0xffu) * scale)) |
-        (static_cast<uint32_t>(f32_to_bf16(e4m3_to_f32(w >> 24) * scale)) << 16);
-  return r;
-}
 
 __device__ __forceinline__ int xcd_remap(int b, int nb) {
   const int q = nb / 8, r = nb % 8;
@@ -274,36 +240,6 @@ struct Layout {
   static constexpr bool A_K = MODE != MODE_WGRAD;
   static constexpr bool B_K = (MODE == MODE_FWD) ? TRANS_B : (MODE == MODE_DGRAD ? !TRANS_B : false);
 };
-
-// Epilogue for a 128x64 wave tile of 32x32 MFMA blocks. D[i][j] of a block
-// sits in lane (j + 32 * ((i / 4) % 2)), register (i % 4) + 4 * (i / 8).
-// Neighbouring lanes swap one value so each lane stores two adjacent
-// columns of one row with a single 4-byte store.
-template <int ET, int FM, int FN>
-__device__ __forceinline__ void store_tile(const f32x16 (&acc)[FM][FN], const TileDesc& t,
-                                           int64_t ri, int64_t cj, int lane) {
-  const int lr = lane & 31, lg = lane >> 5;
-  const bool odd = lr & 1;
-#pragma unroll
-  for (int mi = 0; mi < FM; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < FN; ++ni) {
-      const int64_t gj = cj + ni * 32 + (lr & ~1);
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float send = odd ? acc[mi][ni][r] : acc[mi][ni][r + 1];
-        const float recv = __shfl_xor(send, 1, TT_WAVE);
-        const float lo = odd ? recv : acc[mi][ni][r];
-        const float hi = odd ? acc[mi][ni][r + 1] : recv;
-        const int64_t gi = ri + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3) + (odd ? 1 : 0);
-        if (gi < t.I && gj < t.J) {
-          const uint32_t packed = static_cast<uint32_t>(Mma<ET>::out(lo)) |
-                                  (static_cast<uint32_t>(Mma<ET>::out(hi)) << 16);
-          *reinterpret_cast<uint32_t*>(t.c + (gi * t.ldc + gj) * 2) = packed;
-        }
-      }
-    }
-}
 
 // ===========================================================================
 // MFMA kernel (bf16 / f16): 256x256x32 block tiles, 4 waves of 128x128.
@@ -634,47 +570,203 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
 }
 
 // ===========================================================================
-// Register-staged kernel (FP8 weights).
+// FP8-weight MFMA kernel (fwd / dgrad): e4m3 weights [E, N, K] with 128x128
+// block scales, bf16 activations. The same 256x256x32 tiles and 4 waves as
+// gmm_mfma_kernel; here every wave loads a quarter of the A tile and a
+// quarter of the e4m3 B tile, then dequantises its own B rows into a bf16 B
+// tile: bf16(f32(q) * f32(scale)) with the hardware e4m3 -> f32 conversion
+// (exact) and round-to-nearest-even, i.e. the rule of the reference's
+// offline dequantiser. The MFMA part then reads bf16 fragments as usual.
 // ===========================================================================
-constexpr int RG_BM = 256, RG_BN = 256, RG_BK = 64, RG_NT = 512;
-constexpr int RG_LDK = RG_BK + 8;                 // padded LDS row (elements)
-constexpr int RG_STAGE = (RG_BM + RG_BN) * RG_LDK;  // elements of one stage
+constexpr int F8_STAGE = DM_TILE + DM_TILE / 2;  // A (bf16) + B (e4m3) of one k-tile
+constexpr int F8_BUF = DM_TILE;                  // one dequantised B tile
+constexpr int F8_LDS = 4 * F8_STAGE + 3 * F8_BUF;
 
-template <int MODE, bool TRANS_B, bool FP8, int ET>
-__global__ __launch_bounds__(RG_NT) void gmm_reg_kernel(
-    const char* __restrict__ p0, const char* __restrict__ p1, const char* __restrict__ scale,
-    int scale_dt, char* __restrict__ out, int64_t M, int64_t K, int64_t N, int E,
-    const int64_t* __restrict__ counts, int tiles_i, int tiles_j) {
-  typedef Layout<MODE, TRANS_B> Lay;
-  constexpr bool A_K = Lay::A_K, B_K = Lay::B_K;
-  constexpr int ESZ = 2;
-  constexpr int WGN = 4, WTM = 128, WTN = 64, FM = WTM / 32, FN = WTN / 32;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
 
-  extern __shared__ __align__(16) char smem[];
-  uint16_t* lds = reinterpret_cast<uint16_t*>(smem);
-  int64_t* row_start = reinterpret_cast<int64_t*>(lds + 2 * RG_STAGE);
+// Barrier that also publishes this wave's LDS stores: wait for them, then
+// s_barrier; the memory clobber keeps the compiler from moving LDS accesses
+// across it.
+#define F8_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// Four e4m3 bytes -> four bf16 (two dwords), each bf16(f32(q) * s).
+__device__ __forceinline__ uint2 deq4(uint32_t q, float s) {
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)q, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)q, true);
+  const bf16x2_t a = {(__bf16)(lo.x * s), (__bf16)(lo.y * s)};
+  const bf16x2_t b = {(__bf16)(hi.x * s), (__bf16)(hi.y * s)};
+  return uint2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+}
+
+template <int MODE, bool KMASK>
+__global__ __launch_bounds__(DM_NT) void gmm_fp8_kernel(const char* __restrict__ p0,
+                                                        const char* __restrict__ qw,
+                                                        const char* __restrict__ scale, int sdt,
+                                                        char* __restrict__ out, int64_t M,
+                                                        int64_t K, int64_t N, int E,
+                                                        const int64_t* __restrict__ counts,
+                                                        int tiles_i, int tiles_j) {
+  static_assert(MODE != MODE_WGRAD, "weights are the B operand");
+  typedef Layout<MODE, true> Lay;  // B: K-major for fwd, MN-major for dgrad
+  constexpr int WT = 128, FM = 4, FN = 4;
+  __shared__ __align__(16) char lds_raw[F8_LDS];
+  extern __shared__ __align__(16) char smem[];  // expert schedule, then scales
+  int64_t* row_start = reinterpret_cast<int64_t*>(smem);
   int* tile_start = reinterpret_cast<int*>(row_start + E + 1);
 
   TileDesc t;
-  if (!describe_tile<RG_NT, RG_BM, RG_BN, MODE, TRANS_B, ESZ, FP8 ? 1 : 2>(
-          p0, p1, out, K, N, E, counts, tiles_i, tiles_j, row_start, tile_start, t))
+  if (!describe_tile<DM_NT, DM_BM, DM_BN, MODE, true, 2, 1>(p0, qw, out, K, N, E, counts, tiles_i,
+                                                             tiles_j, row_start, tile_start, t))
     return;
-  const char* abase = t.a;
-  const char* bbase = t.b;
-  const int64_t lda = t.lda, ldb = t.ldb, I = t.I, J = t.J, R = t.R, i0 = t.i0, j0 = t.j0;
-  // Last loadable A row relative to the segment (fwd/dgrad).
-  const int64_t a_clamp = M - 1 - t.seg0;
-  const int64_t a_rows = (MODE == MODE_WGRAD) ? I : t.nrows;
-  const int64_t b_clamp = B_K ? (J - 1) : -1;
 
-  // FP8 block scales of this expert.
-  const char* sbase = nullptr;
-  int64_t sld = 0;
-  if constexpr (FP8) {
-    sld = (K + 127) / 128;
-    sbase = scale + (int64_t)t.e * ((N + 127) / 128) * sld * (scale_dt == TT_F32 ? 4 : 2);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nkt = (int)((t.R + DM_BK - 1) / DM_BK);
+  lds_char* const lds = (lds_char*)lds_raw;
+  lds_char* const bufs = lds + 4 * F8_STAGE;
+
+  // Block scales this tile needs, as f32 in LDS: fwd, scale rows of the two
+  // 128-column blocks of the tile, all k-blocks; dgrad, the two 128-column
+  // (k') blocks, all n-blocks. sc[b * nsc + i], b = block within the tile.
+  const int64_t sld = (K + 127) / 128, snb = (N + 127) / 128;
+  const int nsc = (int)(MODE == MODE_FWD ? sld : snb);
+  float* sc = reinterpret_cast<float*>(tile_start + E + 1 + 2 * E);
+  {
+    const int64_t eoff = (int64_t)t.e * snb * sld;
+    const int64_t b0 = t.j0 / 128;  // first 128-block of the tile's columns
+    for (int idx = threadIdx.x; idx < 2 * nsc; idx += DM_NT) {
+      const int b = idx / nsc, i = idx % nsc;
+      const int64_t blk = b0 + b;
+      int64_t off;
+      if (MODE == MODE_FWD) off = eoff + (blk < snb ? blk : snb - 1) * sld + i;   // [n-block][k-block]
+      else off = eoff + (int64_t)i * sld + (blk < sld ? blk : sld - 1);            // [n-block][k'-block]
+      sc[idx] = sdt == TT_F32 ? reinterpret_cast<const float*>(scale)[off]
+                              : bf16_to_f32(reinterpret_cast<const uint16_t*>(scale)[off]);
+    }
+    __syncthreads();
   }
 
+  // ---- DMA plan: A rows 64w .. 64w + 63 (4 chunks), B e4m3 quarter (2).
+  const i32x4 rsa = make_rsrc(t.a, t.nrows * t.lda * 2);
+  const i32x4 rsb = make_rsrc(t.b, N * K);
+  uint32_t va[4], vb[2];
+  int kofa;
+  const int ca = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t r = t.i0 + 64 * wave + 16 * q + (lane >> 2);
+    va[q] = (uint32_t)((r * t.lda + 8 * ca) * 2);
+  }
+  kofa = 8 * ca;
+  uint32_t kstep_b;
+  int kofb;
+  if constexpr (MODE == MODE_FWD) {
+    // e4m3 rows j (K bytes each): chunk u covers rows 64w + 32u .. + 31,
+    // lane l -> row + l / 2, bytes 16 (l & 1) .. + 15 of the k-tile.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t r = t.j0 + 64 * wave + 32 * u + (lane >> 1);
+      vb[u] = (uint32_t)(r * K + 16 * (lane & 1));
+    }
+    kstep_b = DM_BK;
+    kofb = 16 * (lane & 1);
+  } else {
+    // e4m3 k-rows n: chunk u covers k-rows 8w + 4u .. + 3, lane l -> k-row
+    // + l / 16, columns 16 (l % 16) .. + 15.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int kr = 8 * wave + 4 * u + (lane >> 4);
+      vb[u] = (uint32_t)(kr * K + t.j0 + 16 * (lane & 15));
+    }
+    kstep_b = (uint32_t)(DM_BK * K);
+    kofb = 0;
+  }
+  const int kvalid = (int)t.R;
+  auto issue_one = [&](lds_char* stg, int kt, int q) {
+    if (q < 4) {
+      uint32_t off = va[q] + (uint32_t)kt * (DM_BK * 2);
+      if (KMASK && kt * DM_BK + kofa >= kvalid) off = DM_OOB;
+      dma16(off, rsa, lds_addr_of(stg) + (uint32_t)(4 * wave + q) * 1024u);
+    } else {
+      uint32_t off = vb[q - 4] + (uint32_t)kt * kstep_b;
+      if (MODE == MODE_FWD && KMASK && kt * DM_BK + kofb >= kvalid) off = DM_OOB;
+      dma16(off, rsb, lds_addr_of(stg) + DM_TILE + (uint32_t)(2 * wave + q - 4) * 1024u);
+    }
+  };
+
+  // ---- Dequantisation of this wave's e4m3 rows of k-tile kt (stage `stg`)
+  // into the bf16 B tile `buf`, in 8 parts of 4 values per lane.
+  uint4 raw[2];
+  float dsc;
+  auto deq_read = [&](lds_char* stg, int kt) {
+    if constexpr (MODE == MODE_FWD) {
+      dsc = sc[(wave >> 1) * nsc + min((kt * DM_BK) / 128, nsc - 1)];
+    } else {
+      dsc = sc[((lane & 7) >> 2) * nsc + min((kt * DM_BK) / 128, nsc - 1)];
+    }
+    if constexpr (MODE == MODE_FWD) {
+      const uint32_t o = (uint32_t)DM_TILE + (uint32_t)(64 * wave + lane) * 32u;
+      raw[0] = read_k(stg, o);
+      raw[1] = read_k(stg, o + 16);
+    } else {
+      const uint32_t o = (uint32_t)DM_TILE + (uint32_t)(8 * wave + (lane >> 3)) * 256u +
+                         (uint32_t)(lane & 7) * 32u;
+      raw[0] = read_k(stg, o);
+      raw[1] = read_k(stg, o + 16);
+    }
+  };
+  uint2 cvt[8];
+  auto deq_part = [&](int part) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(raw);
+    cvt[part] = deq4(w[part], dsc);
+  };
+  auto deq_write = [&](lds_char* buf, int half) {
+    // 16 values = 2 x 16 bytes per half.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c16 = 2 * half + i;  // 8-value chunk of this lane's 32 values
+      const uint4 v = uint4{cvt[2 * c16].x, cvt[2 * c16].y, cvt[2 * c16 + 1].x, cvt[2 * c16 + 1].y};
+      uint32_t o;
+      if constexpr (MODE == MODE_FWD) {
+        const int r = 64 * wave + lane;  // B row j, K-major: 64 bytes, chunk c16
+        o = (uint32_t)(r * 64 + ((c16 ^ ((r >> 2) & 3)) << 4));
+      } else {
+        const int kr = 8 * wave + (lane >> 3);
+        const int ch = 4 * (lane & 7) + c16;  // 8-column chunk
+        o = (uint32_t)(kr * 512 + ((ch ^ (4 * (kr & 3))) << 4));
+      }
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(buf + o) =
+          u32x4{v.x, v.y, v.z, v.w};
+    }
+  };
+
+  // ---- Fragments.
+  uint32_t a_off[2], b_off[2], b_mn[FN];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    a_off[s] = fragk_base(wm * WT, s, lane);
+    b_off[s] = fragk_base(wn * WT, s, lane);
+  }
+#pragma unroll
+  for (int ni = 0; ni < FN; ++ni) b_mn[ni] = fragmn_base(wn * WT + ni * 32, lane);
+  uint32_t ao[2], bo[2], bm[FN];
+  auto refresh = [&]() {
+    ao[0] = a_off[0]; ao[1] = a_off[1]; bo[0] = b_off[0]; bo[1] = b_off[1];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) bm[i] = b_mn[i];
+    asm volatile("" : "+v"(ao[0]), "+v"(ao[1]));
+    if constexpr (Lay::B_K) asm volatile("" : "+v"(bo[0]), "+v"(bo[1]));
+    else asm volatile("" : "+v"(bm[0]), "+v"(bm[1]), "+v"(bm[2]), "+v"(bm[3]));
+  };
+  auto frag = [&](lds_char* stg, lds_char* buf, int s, int i, uint4 (&fa)[FM], uint4 (&fb)[FN]) {
+    if (i < FM)
+      fa[i] = read_k(stg, ao[s] + i * 2048);
+    else
+      fb[i - FM] = Lay::B_K ? read_k(buf, bo[s] + (i - FM) * 2048)
+                            : read_mn(buf, bm[i - FM] + s * 8192);
+  };
   f32x16 acc[FM][FN];
 #pragma unroll
   for (int mi = 0; mi < FM; ++mi)
@@ -682,183 +774,74 @@ __global__ __launch_bounds__(RG_NT) void gmm_reg_kernel(
     for (int ni = 0; ni < FN; ++ni)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
-
-  const int tid = threadIdx.x;
-  const int nkt = (int)((R + RG_BK - 1) / RG_BK);
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave / WGN, wn = wave % WGN;
-  const int lr = lane & 31, lg = lane >> 5;
-
-  // Staging: the first half of the block moves the A tile, the second half
-  // the B tile (wave-uniform split); each thread holds eight 16-byte slots:
-  // eight K-major chunks or one 8x8 MN-major micro-tile.
-  constexpr int SH = RG_NT / 2;
-  static_assert(RG_BM * RG_BK / 8 == 8 * SH && RG_BN * RG_BK / 8 == 8 * SH, "staging split");
-  const bool stage_a = tid < SH;
-  const int st = stage_a ? tid : tid - SH;
-  constexpr int KC = RG_BK / 8;
-  uint4 rs[8];
-  uint2 rs8[8];  // raw e4m3 bytes of the B tile (FP8 weights)
-
-  auto scale_at = [&](int64_t n_out, int64_t k_in) -> float {
-    const int64_t si = (n_out >> 7) * sld + (k_in >> 7);
-    return scale_dt == TT_F32 ? reinterpret_cast<const float*>(sbase)[si]
-                              : bf16_to_f32(reinterpret_cast<const uint16_t*>(sbase)[si]);
+  auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
+    acc[i / FN][i % FN] = Mma<TT_BF16>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
   };
 
-  auto load_stage = [&](int kt) {
-    const int64_t k0 = (int64_t)kt * RG_BK;
-    if (stage_a) {
-      if constexpr (A_K) {
+  lds_char* const s0 = lds;
+  lds_char* const s1 = lds + F8_STAGE;
+  lds_char* const s2 = lds + 2 * F8_STAGE;
+  lds_char* const s3 = lds + 3 * F8_STAGE;
+  auto buf_of = [&](int kt) { return bufs + (kt % 3) * F8_BUF; };
+  uint4 a0[FM], b0[FN], a1[FM], b1[FN];
+
+  // k-tile kt: wait for this wave's loads of k-tile kt+1; multiply k-step 0
+  // while reading k-step 1 and dequantising this wave's rows of k-tile kt+1;
+  // barrier (k-tile kt+1 complete in LDS, A and bf16 B); multiply k-step 1
+  // while reading k-step 0 of k-tile kt+1 and loading k-tile kt+3 into the
+  // stage of k-tile kt-1. Three bf16 B tiles rotate, so a tile is rewritten
+  // only after every wave has finished the k-tile before.
+  auto step = [&](int kt, lds_char* cur, lds_char* nxt, lds_char* refill) {
+    lds_char* const bc = buf_of(kt);
+    lds_char* const bn = buf_of(kt + 1);
+    TT_WAIT_VMCNT(6);
+    refresh();
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = st + SH * q;
-          const int r = c / KC, kc = c % KC;
-          // Rows past the segment belong to later experts (or are clamped to
-          // the last row); their products only reach rows that are not stored.
-          int64_t gr = i0 + r;
-          if (gr > a_clamp) gr = a_clamp;
-          const int64_t gk = k0 + kc * 8;
-          rs[q] = gk < R ? *reinterpret_cast<const uint4*>(abase + (gr * lda + gk) * ESZ)
-                         : make_uint4(0, 0, 0, 0);
-        }
-      } else {
-        const int kg = st % KC, rg = st / KC;  // lanes walk k: conflict-free LDS rows
-        const int64_t gr = i0 + rg * 8;
+    for (int i = 0; i < FM * FN; ++i) {
+      mfma(i, a0, b0);
+      if (i < FM + FN) frag(cur, bc, 1, i, a1, b1);
+      if (i == 1) deq_read(nxt, kt + 1);
+      if (i >= 4 && i < 12) deq_part(i - 4);
+      if (i == 8) deq_write(bn, 0);
+      if (i == 12) deq_write(bn, 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    F8_BARRIER();
+    refresh();
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const int64_t gk = k0 + kg * 8 + kk;
-          const bool ok = gr < a_rows && gk < R;
-          rs[kk] = ok ? *reinterpret_cast<const uint4*>(abase + (gk * lda + gr) * ESZ)
-                      : make_uint4(0, 0, 0, 0);
-        }
-      }
-    } else {
-      if constexpr (B_K) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = st + SH * q;
-          const int r = c / KC, kc = c % KC;
-          int64_t gj = j0 + r;
-          if (gj > b_clamp) gj = b_clamp;
-          const int64_t gk = k0 + kc * 8;
-          const bool ok = gk < R;
-          if constexpr (FP8)
-            rs8[q] = ok ? *reinterpret_cast<const uint2*>(bbase + gj * ldb + gk) : make_uint2(0, 0);
-          else
-            rs[q] = ok ? *reinterpret_cast<const uint4*>(bbase + (gj * ldb + gk) * ESZ)
-                       : make_uint4(0, 0, 0, 0);
-        }
-      } else {
-        const int kg = st % KC, rg = st / KC;
-        const int64_t gj = j0 + rg * 8;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const int64_t gk = k0 + kg * 8 + kk;
-          const bool ok = gj < J && gk < R;
-          if constexpr (FP8)
-            rs8[kk] = ok ? *reinterpret_cast<const uint2*>(bbase + gk * ldb + gj) : make_uint2(0, 0);
-          else
-            rs[kk] = ok ? *reinterpret_cast<const uint4*>(bbase + (gk * ldb + gj) * ESZ)
-                        : make_uint4(0, 0, 0, 0);
-        }
-      }
+    for (int i = 0; i < FM * FN; ++i) {
+      mfma(i, a1, b1);
+      if (i < FM + FN) frag(nxt, bn, 0, i, a0, b0);
+      if (i < 6) issue_one(refill, kt + 3, i);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  auto store_stage = [&](int kt, uint16_t* stage) {
-    const int64_t k0 = (int64_t)kt * RG_BK;
-    if (stage_a) {
-      if constexpr (A_K) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = st + SH * q;
-          const int r = c / KC, kc = c % KC;
-          *reinterpret_cast<uint4*>(stage + r * RG_LDK + kc * 8) = rs[q];
-        }
-      } else {
-        const int kg = st % KC, rg = st / KC;
-        uint4 tr[8];
-        transpose8x8(rs, tr);
+  for (int q = 0; q < 6; ++q) issue_one(s0, 0, q);
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
-          *reinterpret_cast<uint4*>(stage + (rg * 8 + rr) * RG_LDK + kg * 8) = tr[rr];
-      }
-    } else {
-      uint16_t* lb = stage + RG_BM * RG_LDK;
-      if constexpr (B_K) {
+  for (int q = 0; q < 6; ++q) issue_one(s1, 1, q);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int c = st + SH * q;
-          const int r = c / KC, kc = c % KC;
-          uint4 val;
-          if constexpr (FP8) {
-            int64_t gj = j0 + r;
-            if (gj > b_clamp) gj = b_clamp;
-            const float s = scale_at(gj, k0 + kc * 8);  // weight [out = j][in = k]
-            const uint2 lo = dequant4(rs8[q].x, s), hi = dequant4(rs8[q].y, s);
-            val = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          } else {
-            val = rs[q];
-          }
-          *reinterpret_cast<uint4*>(lb + r * RG_LDK + kc * 8) = val;
-        }
-      } else {
-        const int kg = st % KC, rg = st / KC;
-        uint4 tr[8];
-        if constexpr (FP8) {
-          // weight [out = k][in = j]: the 8 rows are 8 consecutive k inside one
-          // 128-block of k, and 8 consecutive j inside one 128-block of j.
-          const int64_t jj = (j0 + rg * 8 < J) ? j0 + rg * 8 : J - 1;  // tiles past J
-          const float s = scale_at(k0 + kg * 8, jj);
-          uint4 in[8];
+  for (int q = 0; q < 6; ++q) issue_one(s2, 2, q);
+  TT_WAIT_VMCNT(12);  // this wave's loads of k-tile 0
+  deq_read(s0, 0);
 #pragma unroll
-          for (int kk = 0; kk < 8; ++kk) {
-            const uint2 lo = dequant4(rs8[kk].x, s), hi = dequant4(rs8[kk].y, s);
-            in[kk] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          }
-          transpose8x8(in, tr);
-        } else {
-          transpose8x8(rs, tr);
-        }
+  for (int part = 0; part < 8; ++part) deq_part(part);
+  deq_write(buf_of(0), 0);
+  deq_write(buf_of(0), 1);
+  F8_BARRIER();
+  refresh();
 #pragma unroll
-        for (int rr = 0; rr < 8; ++rr)
-          *reinterpret_cast<uint4*>(lb + (rg * 8 + rr) * RG_LDK + kg * 8) = tr[rr];
-      }
-    }
-  };
-
-  // Pipeline: global loads of tile k+1 are in flight while tile k is
-  // multiplied out of one LDS stage; they land in the other stage afterwards.
-  // One barrier per k-tile.
-  if (nkt > 0) {
-    load_stage(0);
-    store_stage(0, lds);
+  for (int i = 0; i < FM + FN; ++i) frag(s0, buf_of(0), 0, i, a0, b0);
+  for (int kt = 0; kt < nkt; kt += DM_ST) {
+    step(kt, s0, s1, s3);
+    if (kt + 1 < nkt) step(kt + 1, s1, s2, s0);
+    if (kt + 2 < nkt) step(kt + 2, s2, s3, s1);
+    if (kt + 3 < nkt) step(kt + 3, s3, s0, s2);
   }
+  TT_WAIT_VMCNT(0);
   __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const uint16_t* cur = lds + (kt & 1) * RG_STAGE;
-    if (kt + 1 < nkt) load_stage(kt + 1);
-    const uint16_t* la = cur + (wm * WTM + lr) * RG_LDK + lg * 8;
-    const uint16_t* lbp = cur + RG_BM * RG_LDK + (wn * WTN + lr) * RG_LDK + lg * 8;
-#pragma unroll
-    for (int s = 0; s < RG_BK / 16; ++s) {
-      uint4 fa[FM], fb[FN];
-#pragma unroll
-      for (int mi = 0; mi < FM; ++mi)
-        fa[mi] = *reinterpret_cast<const uint4*>(la + mi * 32 * RG_LDK + s * 16);
-#pragma unroll
-      for (int ni = 0; ni < FN; ++ni)
-        fb[ni] = *reinterpret_cast<const uint4*>(lbp + ni * 32 * RG_LDK + s * 16);
-#pragma unroll
-      for (int mi = 0; mi < FM; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < FN; ++ni) acc[mi][ni] = Mma<ET>::run(fa[mi], fb[ni], acc[mi][ni]);
-    }
-    if (kt + 1 < nkt) store_stage(kt + 1, lds + ((kt + 1) & 1) * RG_STAGE);
-    __syncthreads();
-  }
-  store_tile<ET, FM, FN>(acc, t, i0 + wm * WTM, j0 + wn * WTN, lane);
+  store_wave_tile<TT_BF16>(acc, t, t.i0 + wm * WT, t.j0 + wn * WT, lane, lds + wave * 32768);
 }
 
 // ---------------------------------------------------------------------------
@@ -1002,23 +985,44 @@ int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K,
   return launch_mfma_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
 }
 
-template <int MODE, bool TB, bool FP8, int ET>
-int launch_reg(const void* p0, const void* p1, const void* scale, int sdt, void* out, int64_t M,
-               int64_t K, int64_t N, int E, const int64_t* counts, hipStream_t s) {
-  int ti, tj;
-  const int64_t nblk = grid_blocks(MODE, TB, M, K, N, E, RG_BM, RG_BN, ti, tj);
-  if (nblk == 0) return TT_OK;
-  TT_REQUIRE(nblk < 0x7fffffff, "gmm: grid too large");
-  const size_t lds = (size_t)2 * RG_STAGE * 2 + schedule_bytes(E);
-  TT_REQUIRE(lds <= 160 * 1024, "gmm: too many experts for the LDS tile schedule");
+template <int MODE, bool KMASK>
+int launch_fp8_k(const void* p0, const uint8_t* qw, const void* scale, int sdt, void* out,
+                 int64_t M, int64_t K, int64_t N, int E, const int64_t* counts, hipStream_t s,
+                 int64_t nblk, int ti, int tj, size_t lds) {
   static size_t allowed = 64 * 1024;
-  const int rc = allow_lds(&gmm_reg_kernel<MODE, TB, FP8, ET>, lds, allowed);
+  const int rc = allow_lds(&gmm_fp8_kernel<MODE, KMASK>, lds, allowed);
   if (rc != TT_OK) return rc;
-  hipLaunchKernelGGL((gmm_reg_kernel<MODE, TB, FP8, ET>), dim3((unsigned)nblk), dim3(RG_NT), lds,
-                     s, static_cast<const char*>(p0), static_cast<const char*>(p1),
+  hipLaunchKernelGGL((gmm_fp8_kernel<MODE, KMASK>), dim3((unsigned)nblk), dim3(DM_NT), lds, s,
+                     static_cast<const char*>(p0), reinterpret_cast<const char*>(qw),
                      static_cast<const char*>(scale), sdt, static_cast<char*>(out), M, K, N, E,
                      counts, ti, tj);
-  return tt_check_launch("gmm");
+  return tt_check_launch("gmm_fp8");
+}
+
+template <int MODE>
+int launch_fp8(const void* p0, const uint8_t* qw, const void* scale, int sdt, void* out, int64_t M,
+               int64_t K, int64_t N, int E, const int64_t* counts, hipStream_t s) {
+  int ti, tj;
+  const int64_t nblk = grid_blocks(MODE, true, M, K, N, E, DM_BM, DM_BN, ti, tj);
+  if (nblk == 0) return TT_OK;
+  TT_REQUIRE(nblk < 0x7fffffff, "gmm_fp8: grid too large");
+  // Dynamic LDS: the expert schedule, then the f32 block scales of the two
+  // 128-column blocks of a tile.
+  const int64_t nsc = MODE == MODE_FWD ? (K + 127) / 128 : (N + 127) / 128;
+  const size_t lds = schedule_bytes(E) + (size_t)(2 * nsc) * sizeof(float);
+  TT_REQUIRE(lds + (size_t)F8_LDS + 64 <= 160 * 1024,
+             "gmm_fp8: too many experts or scale blocks for LDS (E=%d, blocks=%lld)", E,
+             (long long)nsc);
+  const int64_t ld = K > N ? K : N;
+  TT_REQUIRE((M + DM_BM) * ld * 2 < (int64_t)DM_OOB && (N + DM_BN) * K < (int64_t)DM_OOB,
+             "gmm_fp8: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
+             (long long)M, (long long)K, (long long)N);
+  const int64_t R = MODE == MODE_FWD ? K : N;
+  if (R % DM_BK)
+    return launch_fp8_k<MODE, true>(p0, qw, scale, sdt, out, M, K, N, E, counts, s, nblk, ti, tj,
+                                    lds);
+  return launch_fp8_k<MODE, false>(p0, qw, scale, sdt, out, M, K, N, E, counts, s, nblk, ti, tj,
+                                   lds);
 }
 
 template <int MODE, bool TB>
@@ -1096,8 +1100,8 @@ extern "C" int tt_gmm_fp8_fwd(const void* x, const uint8_t* qw, const void* scal
                               int32_t num_experts, const int64_t* counts, void* y, void* stream) {
   const int rc = fp8_checks(x, qw, y, scale_dtype, m, k, n, num_experts);
   if (rc != TT_OK) return rc;
-  return launch_reg<MODE_FWD, true, true, TT_BF16>(x, qw, scale, scale_dtype, y, m, k, n,
-                                                   num_experts, counts, S(stream));
+  return launch_fp8<MODE_FWD>(x, qw, scale, scale_dtype, y, m, k, n, num_experts, counts,
+                             S(stream));
 }
 
 extern "C" int tt_gmm_fp8_dgrad(const void* dy, const uint8_t* qw, const void* scale,
@@ -1106,6 +1110,6 @@ extern "C" int tt_gmm_fp8_dgrad(const void* dy, const uint8_t* qw, const void* s
                                 void* stream) {
   const int rc = fp8_checks(dy, qw, dx, scale_dtype, m, k, n, num_experts);
   if (rc != TT_OK) return rc;
-  return launch_reg<MODE_DGRAD, true, true, TT_BF16>(dy, qw, scale, scale_dtype, dx, m, k, n,
-                                                     num_experts, counts, S(stream));
+  return launch_fp8<MODE_DGRAD>(dy, qw, scale, scale_dtype, dx, m, k, n, num_experts, counts,
+                               S(stream));
 }
