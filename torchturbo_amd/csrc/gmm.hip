@@ -21,7 +21,15 @@
 //   gfx950 transposing load ds_read_b64_tr_b16 (no register transpose).
 //   MFMAs, fragment reads of the next k-step and DMA issue are interleaved
 //   one per slot. The epilogue converts to 16 bits in hardware and stores
-//   through LDS as full 256-byte rows.
+//   through LDS as full 256-byte rows. Serves wgrad and short reductions.
+// * gmm_p64_kernel (bf16/f16 fwd/dgrad with a reduction longer than 64):
+//   persistent, one block per CU walking a strided list of output tiles;
+//   256x256x64 tiles through two 64 KiB LDS stages, so K-major rows are
+//   whole 128-byte lines. The k-tiles of consecutive tiles form one stream
+//   (the next tile's first loads overlap the current tile's last k-tile and
+//   epilogue); the epilogue stages through a private 4 KiB of LDS per wave
+//   and stores with buffer stores whose resource ends at the expert's last
+//   row.
 // * gmm_fp8_kernel (fwd/dgrad with e4m3 weights and 128x128 block scales):
 //   the same tiles and pipeline; the weight tile arrives in LDS as e4m3
 //   bytes and each wave decodes its own rows in hardware, multiplies by the
@@ -37,6 +45,8 @@
 // take experts longest-first and are left in hardware round-robin order, so
 // the tiles of a heavily loaded expert spread over all XCDs.
 #include "common.h"
+
+#include <type_traits>
 
 namespace {
 
@@ -569,6 +579,354 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   store_wave_tile<ET>(acc, t, t.i0 + wm * WT, t.j0 + wn * WT, lane, region);
 }
 
+// Barrier that also publishes this wave's LDS stores and retires its LDS
+// reads: wait for them, then s_barrier; the memory clobber keeps the
+// compiler from moving LDS accesses across it. Loads in flight (vmcnt) are
+// not waited for.
+#define TT_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+__device__ __forceinline__ int64_t rfl64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Output tile L (fwd / dgrad) from the schedule in LDS.
+template <int MODE, bool TRANS_B, int ESZ>
+__device__ __forceinline__ void tile_at(int L, const char* p0, const char* p1, char* out,
+                                        int64_t K, int64_t N, int E, int tiles_j,
+                                        const int64_t* row_start, const int* tile_start,
+                                        TileDesc& t) {
+  const int slot = L / tiles_j, jt = L % tiles_j;
+  int lo = 0, hi = E - 1;  // last e with tile_start[e] <= slot
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tile_start[mid] <= slot) lo = mid; else hi = mid - 1;
+  }
+  // Schedule values are uniform: keep them (and all that derives from them)
+  // in scalar registers.
+  const int e = __builtin_amdgcn_readfirstlane(lo);
+  t.e = e;
+  t.seg0 = rfl64(row_start[e]);
+  t.nrows = rfl64(row_start[e + 1]) - t.seg0;
+  const int ts_e = __builtin_amdgcn_readfirstlane(tile_start[e]);
+  if constexpr (MODE == MODE_FWD) {
+    t.a = p0 + t.seg0 * K * ESZ; t.lda = K;
+    t.b = p1 + (int64_t)e * K * N * ESZ; t.ldb = TRANS_B ? K : N;
+    t.I = t.nrows; t.J = N; t.R = K;
+    t.c = out + t.seg0 * N * ESZ; t.ldc = N;
+  } else {
+    t.a = p0 + t.seg0 * N * ESZ; t.lda = N;
+    t.b = p1 + (int64_t)e * K * N * ESZ; t.ldb = TRANS_B ? K : N;
+    t.I = t.nrows; t.J = K; t.R = N;
+    t.c = out + t.seg0 * K * ESZ; t.ldc = K;
+  }
+  t.i0 = (int64_t)(slot - ts_e) * DM_BM;
+  t.j0 = (int64_t)jt * DM_BN;
+}
+
+// ===========================================================================
+// Persistent MFMA kernel (fwd / dgrad, bf16 / f16): one block per CU walks a
+// strided list of 256x256 output tiles and streams their 64-deep k-tiles as
+// one sequence through two LDS stages, so a tile's first k-tiles are already
+// loading while the previous tile finishes and its epilogue runs; the
+// expert schedule is built once per block. Tile L of a launch (slot-major,
+// n-tile minor) goes to block position L % G, positions XCD-grouped, so the
+// CUs of one XCD work on consecutive tiles (shared A panels and weights).
+// ===========================================================================
+// 256x256x64 tiles, two 64 KiB LDS stages (A 32 KiB, B 32 KiB). K-major rows
+// are 128 bytes per k-tile, so every load covers whole 128-byte lines.
+constexpr int P_BK = 64;
+constexpr int P_OPND = 256 * P_BK * 2;  // one operand tile (32 KiB)
+constexpr int P_STAGE = 2 * P_OPND;     // A then B
+constexpr int P_EPI = 4096;             // epilogue staging per wave
+
+// K-major 64-deep tile: LDS row r (128 bytes) holds tile row r, its 16-byte
+// chunk c in slot c ^ (r & 7). Fragment for k-step s (0..3): rows
+// r0 + lane % 32, chunk 2 s + lane / 32; further 32-row blocks add 4096.
+__device__ __forceinline__ uint32_t fragk64(int r0, int s, int lane) {
+  const int r = r0 + (lane & 31);
+  const int c = 2 * s + (lane >> 5);
+  return (uint32_t)(r * 128 + ((c ^ (r & 7)) << 4));
+}
+
+// Epilogue of the 64-deep kernel: the wave's 128x128 tile in 8 rounds of
+// 32 rows x 64 columns through its private 4 KiB of LDS (row r at 128 r,
+// 16-byte chunk c in slot c ^ (r & 7)), stored as 128-byte row segments with
+// buffer stores. The store resource ends at the expert's last row, so
+// stores to rows past it are dropped by the hardware; columns past the
+// output width are given an offset past the resource.
+template <int ET>
+__device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], const TileDesc& t,
+                                                    int64_t ri, int64_t cj, lds_char* region) {
+  // Lane index computed here (volatile, so neither it nor what derives from
+  // it is hoisted into registers that stay live across the k-loop).
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  // The accumulator reads below are inline assembly, which the compiler's
+  // hazard padding does not cover: wait out the MFMA write-to-read latency.
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  const int64_t rows = t.I - ri;
+  const int64_t obytes = rows > 0 ? rows * t.ldc * 2 - cj * 2 : 0;
+  const uint32_t nrec = obytes < (int64_t)DM_OOB ? (uint32_t)obytes : DM_OOB;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(t.c + (ri * t.ldc + cj) * 2), (short)0, (int)nrec, 0x00020000);
+  const uint32_t row_bytes = (uint32_t)(t.ldc * 2);
+  const int r_l = lane & 31, h = lane >> 5;
+  const int rr = lane >> 3, ch = lane & 7;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int nh = 0; nh < 2; ++nh) {
+#pragma unroll
+      for (int nn = 0; nn < 2; ++nn)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ni = 2 * nh + nn;
+          const int c = 4 * nn + g;
+          // Accumulators are read out of the AGPRs four at a time, where they
+          // are converted (a bulk copy would need the whole register file).
+          float x0, x1, x2, x3;
+          asm volatile("v_accvgpr_read_b32 %0, %4\n\tv_accvgpr_read_b32 %1, %5\n\t"
+                       "v_accvgpr_read_b32 %2, %6\n\tv_accvgpr_read_b32 %3, %7"
+                       : "=v"(x0), "=v"(x1), "=v"(x2), "=v"(x3)
+                       : "a"(acc[mi][ni][4 * g]), "a"(acc[mi][ni][4 * g + 1]),
+                         "a"(acc[mi][ni][4 * g + 2]), "a"(acc[mi][ni][4 * g + 3]));
+          const uint2 v = pack4<ET>(x0, x1, x2, x3);
+          *reinterpret_cast<lds_u32x2*>(region + r_l * 128 + ((c ^ (r_l & 7)) << 4) + 8 * h) =
+              u32x2{v.x, v.y};
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      const int64_t col = 64 * nh + 8 * ch;
+      const bool col_ok = cj + col < t.J;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 8 * q + rr;
+        const uint4 v = read_k(region, (uint32_t)(r * 128 + ((ch ^ (r & 7)) << 4)));
+        const uint32_t off = col_ok ? (uint32_t)(32 * mi + r) * row_bytes + (uint32_t)col * 2u
+                                    : DM_OOB;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (int)off, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int MODE, bool TRANS_B, int ET, bool KMASK>
+__global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__ p0,
+                                                        const char* __restrict__ p1,
+                                                        char* __restrict__ out, int64_t M,
+                                                        int64_t K, int64_t N, int E,
+                                                        const int64_t* __restrict__ counts,
+                                                        int tiles_j) {
+  static_assert(MODE != MODE_WGRAD, "fwd / dgrad only");
+  typedef Layout<MODE, TRANS_B> Lay;
+  constexpr int WT = 128, FM = 4, FN = 4;
+  __shared__ __align__(16) char lds_raw[2 * P_STAGE];
+  __shared__ __align__(16) char epi_raw[4 * P_EPI];
+  extern __shared__ __align__(16) char smem[];  // expert schedule
+  int64_t* row_start = reinterpret_cast<int64_t*>(smem);
+  int* tile_start = reinterpret_cast<int*>(row_start + E + 1);
+  scan_counts<DM_NT>(counts, E, DM_BM, row_start, tile_start);
+
+  const int G = gridDim.x;
+  const int pos = xcd_remap(blockIdx.x, G);
+  const int total = tile_start[E] * tiles_j;
+  if (pos >= total) return;
+  const int ntiles = (total - pos + G - 1) / G;
+  const int64_t R = MODE == MODE_FWD ? K : N;
+  const int nkt = (int)((R + P_BK - 1) / P_BK);  // >= 2 (host check)
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t lda = MODE == MODE_FWD ? K : N;
+  const int64_t ldb = TRANS_B ? K : N;
+
+  // Loads: every wave brings 8 KiB of A (chunks 0-7) and 8 KiB of B (8-15)
+  // per k-tile, 1 KiB per instruction. K-major: rows 64 w + 8 q + lane / 8,
+  // slot lane % 8; MN-major: k-rows 16 w + 2 q + lane / 32, slot lane % 32.
+  // Offsets are relative to the tile origin (the resource base); chunk q
+  // adds a uniform q * qstep to the chunk-0 offset.
+  // MN-major: the slot swizzle depends on k-row & 3, which alternates
+  // between even and odd chunks, so odd chunks have a base of their own.
+  uint32_t vbase[2], vodd[2], qstep[2], kstep[2];
+  int kof = 0;
+#pragma unroll
+  for (int op = 0; op < 2; ++op) {
+    const bool kmaj = op == 0 ? Lay::A_K : Lay::B_K;
+    const int64_t ld = op == 0 ? lda : ldb;
+    if (kmaj) {
+      const int r = 64 * wave + (lane >> 3);
+      const int c = (lane & 7) ^ ((lane >> 3) & 7);
+      vbase[op] = (uint32_t)(((int64_t)r * ld + 8 * c) * 2);
+      vodd[op] = vbase[op];
+      qstep[op] = (uint32_t)(8 * ld * 2);
+      kstep[op] = P_BK * 2;
+      kof = 8 * c;
+    } else {
+      const int kr = 16 * wave + (lane >> 5);
+      const int c = (lane & 31) ^ (4 * (kr & 3));
+      const int c1 = (lane & 31) ^ (4 * ((kr + 2) & 3));
+      vbase[op] = (uint32_t)(((int64_t)kr * ld + 8 * c) * 2);
+      vodd[op] = (uint32_t)(((int64_t)(kr + 2) * ld + 8 * c1) * 2);
+      qstep[op] = (uint32_t)(4 * ld * 2);  // per pair of chunks
+      kstep[op] = (uint32_t)(P_BK * ld * 2);
+    }
+  }
+
+  auto rsrc_a = [&](const TileDesc& t, bool valid) -> i32x4 {
+    if (!valid) return make_rsrc(p0, 0);
+    const int64_t toff = t.i0 * t.lda * 2;  // A is K-major in fwd / dgrad
+    return make_rsrc(t.a + toff, t.nrows * t.lda * 2 - toff);
+  };
+  auto rsrc_b = [&](const TileDesc& t, bool valid) -> i32x4 {
+    if (!valid) return make_rsrc(p0, 0);
+    const int64_t toff = Lay::B_K ? t.j0 * t.ldb * 2 : t.j0 * 2;
+    return make_rsrc(t.b + toff, K * N * 2 - toff);
+  };
+
+  TileDesc tc, tn;
+  tile_at<MODE, TRANS_B, 2>(pos, p0, p1, out, K, N, E, tiles_j, row_start, tile_start, tc);
+  if (ntiles > 1)
+    tile_at<MODE, TRANS_B, 2>(pos + G, p0, p1, out, K, N, E, tiles_j, row_start, tile_start, tn);
+  i32x4 ra_cur = rsrc_a(tc, true), rb_cur = rsrc_b(tc, true);
+  i32x4 ra_nxt = rsrc_a(tn, ntiles > 1), rb_nxt = rsrc_b(tn, ntiles > 1);
+  const int kvalid = (int)R;
+
+  // Chunk q (0-7 A, 8-15 B) of k-tile k of the current or next tile.
+  auto issue_one = [&](lds_char* stg, int k, bool nxt, int q) {
+    const bool is_a = q < 8;
+    const int op = is_a ? 0 : 1;
+    const bool kmaj = is_a ? Lay::A_K : Lay::B_K;
+    const int qq = q & 7;
+    uint32_t vb = (!kmaj && (qq & 1)) ? vodd[op] : vbase[op];
+    asm volatile("" : "+v"(vb));  // one register per base, not one per chunk
+    const uint32_t qi = kmaj ? (uint32_t)qq : (uint32_t)(qq >> 1);
+    uint32_t off = vb + (qi * qstep[op] + (uint32_t)k * kstep[op]);
+    if constexpr (KMASK) {
+      if (kmaj && k * P_BK + kof >= kvalid) off = DM_OOB;
+    }
+    const i32x4 rs = is_a ? (nxt ? ra_nxt : ra_cur) : (nxt ? rb_nxt : rb_cur);
+    dma16(off, rs, lds_addr_of(stg) + (is_a ? 0u : (uint32_t)P_OPND) +
+                       (uint32_t)(8 * wave + (q & 7)) * 1024u);
+  };
+
+  uint32_t a_k[4], b_k[4], a_mn[FM], b_mn[FN];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    a_k[s] = fragk64(wm * WT, s, lane);
+    b_k[s] = fragk64(wn * WT, s, lane) + P_OPND;
+  }
+#pragma unroll
+  for (int mi = 0; mi < FM; ++mi) a_mn[mi] = fragmn_base(wm * WT + mi * 32, lane);
+#pragma unroll
+  for (int ni = 0; ni < FN; ++ni) b_mn[ni] = fragmn_base(wn * WT + ni * 32, lane) + P_OPND;
+
+  f32x16 acc[FM][FN];
+  uint32_t ao, bo, am[FM], bm[FN];
+  // Offsets for k-step s, re-materialised per use (one register each).
+  auto refresh = [&](int s) {
+    ao = a_k[s]; bo = b_k[s];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) am[i] = a_mn[i];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) bm[i] = b_mn[i];
+    if constexpr (Lay::A_K) asm volatile("" : "+v"(ao));
+    else asm volatile("" : "+v"(am[0]), "+v"(am[1]), "+v"(am[2]), "+v"(am[3]));
+    if constexpr (Lay::B_K) asm volatile("" : "+v"(bo));
+    else asm volatile("" : "+v"(bm[0]), "+v"(bm[1]), "+v"(bm[2]), "+v"(bm[3]));
+  };
+  auto frag = [&](lds_char* stg, int s, int i, uint4 (&fa)[FM], uint4 (&fb)[FN]) {
+    if (i < FM)
+      fa[i] = Lay::A_K ? read_k(stg, ao + i * 4096) : read_mn(stg, am[i] + s * 8192);
+    else
+      fb[i - FM] = Lay::B_K ? read_k(stg, bo + (i - FM) * 4096)
+                            : read_mn(stg, bm[i - FM] + s * 8192);
+  };
+  auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
+    acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
+  };
+
+  lds_char* const lds = (lds_char*)lds_raw;
+  auto stage = [&](int g) { return lds + (g & 1) * P_STAGE; };
+  uint4 a0[FM], b0[FN], a1[FM], b1[FN];
+
+  // One k-tile: k-steps 0-2 multiply while reading the next k-step; then
+  // wait for k-tile kt + 1 (the only load in flight), barrier (every wave is
+  // past its reads of this stage), and k-step 3 multiplies while reading
+  // k-step 0 of k-tile kt + 1 and loading k-tile kt + 2 into this stage.
+  auto step = [&](int kt, int g, auto last_c) {
+    constexpr bool LAST = decltype(last_c)::value;
+    lds_char* const cur = stage(g);
+    lds_char* const nxt = stage(g + 1);
+    const int k2 = kt + 2;
+    const bool to_next = k2 >= nkt;
+    const int kr = to_next ? k2 - nkt : k2;
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      refresh(s + 1);
+#pragma unroll
+      for (int i = 0; i < FM * FN; ++i) {
+        if (s & 1) mfma(i, a1, b1); else mfma(i, a0, b0);
+        if (i < FM + FN) {
+          if (s & 1) frag(cur, s + 1, i, a0, b0); else frag(cur, s + 1, i, a1, b1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    TT_WAIT_VMCNT(0);
+    TT_LDS_BARRIER();
+    refresh(0);
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+      mfma(i, a1, b1);
+      if (!LAST && i < FM + FN) frag(nxt, 0, i, a0, b0);
+      issue_one(cur, kr, to_next, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+#pragma unroll
+  for (int q = 0; q < 16; ++q) issue_one(stage(0), 0, false, q);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) issue_one(stage(1), 1, false, q);
+  TT_WAIT_VMCNT(16);
+  __builtin_amdgcn_s_barrier();
+  refresh(0);
+#pragma unroll
+  for (int i = 0; i < FM + FN; ++i) frag(stage(0), 0, i, a0, b0);
+
+  lds_char* const epi = (lds_char*)epi_raw + wave * P_EPI;
+  int g = 0;
+  for (int n = 0;;) {
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+    for (int kt = 0; kt < nkt - 1; ++kt, ++g) step(kt, g, std::false_type{});
+    step(nkt - 1, g, std::true_type{});
+    ++g;
+    __builtin_amdgcn_sched_barrier(0);
+    store_wave_tile_p64<ET>(acc, tc, tc.i0 + wm * WT, tc.j0 + wn * WT, epi);
+    if (++n == ntiles) break;
+    tc = tn;
+    ra_cur = ra_nxt;
+    rb_cur = rb_nxt;
+    const bool more = n + 1 < ntiles;
+    if (more)
+      tile_at<MODE, TRANS_B, 2>(pos + (n + 1) * G, p0, p1, out, K, N, E, tiles_j, row_start,
+                                tile_start, tn);
+    ra_nxt = rsrc_a(tn, more);
+    rb_nxt = rsrc_b(tn, more);
+    refresh(0);
+#pragma unroll
+    for (int i = 0; i < FM + FN; ++i) frag(stage(g), 0, i, a0, b0);
+  }
+  TT_WAIT_VMCNT(0);  // loads issued past the last tile land before the block exits
+}
+
 // ===========================================================================
 // FP8-weight MFMA kernel (fwd / dgrad): e4m3 weights [E, N, K] with 128x128
 // block scales, bf16 activations. The same 256x256x32 tiles and 4 waves as
@@ -584,10 +942,6 @@ constexpr int F8_LDS = 4 * F8_STAGE + 3 * F8_BUF;
 
 typedef __attribute__((ext_vector_type(2))) float f32x2;
 
-// Barrier that also publishes this wave's LDS stores: wait for them, then
-// s_barrier; the memory clobber keeps the compiler from moving LDS accesses
-// across it.
-#define F8_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
 // Four e4m3 bytes -> four bf16 (two dwords), each bf16(f32(q) * s).
@@ -806,7 +1160,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_fp8_kernel(const char* __restrict__
       if (i == 12) deq_write(bn, 1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    F8_BARRIER();
+    TT_LDS_BARRIER();
     refresh();
 #pragma unroll
     for (int i = 0; i < FM * FN; ++i) {
@@ -829,7 +1183,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_fp8_kernel(const char* __restrict__
   for (int part = 0; part < 8; ++part) deq_part(part);
   deq_write(buf_of(0), 0);
   deq_write(buf_of(0), 1);
-  F8_BARRIER();
+  TT_LDS_BARRIER();
   refresh();
 #pragma unroll
   for (int i = 0; i < FM + FN; ++i) frag(s0, buf_of(0), 0, i, a0, b0);
@@ -963,6 +1317,37 @@ int launch_mfma_k(const void* p0, const void* p1, void* out, int64_t M, int64_t 
   return tt_check_launch("gmm");
 }
 
+// Compute units of the current device (the persistent kernel's grid), cached
+// per device.
+int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int MODE, bool TB, int ET, bool KMASK>
+int launch_p64_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
+                 int E, const int64_t* counts, hipStream_t s, int64_t nblk, int tj) {
+  const size_t lds = schedule_bytes(E);  // stages and epilogue staging are static LDS
+  static size_t allowed = 64 * 1024;
+  const int rc = allow_lds(&gmm_p64_kernel<MODE, TB, ET, KMASK>, lds, allowed);
+  if (rc != TT_OK) return rc;
+  const int64_t cus = cu_count();
+  const int64_t grid = nblk < cus ? nblk : cus;
+  hipLaunchKernelGGL((gmm_p64_kernel<MODE, TB, ET, KMASK>), dim3((unsigned)grid), dim3(DM_NT),
+                     lds, s, static_cast<const char*>(p0), static_cast<const char*>(p1),
+                     static_cast<char*>(out), M, K, N, E, counts, tj);
+  return tt_check_launch("gmm");
+}
+
 template <int MODE, bool TB, int ET>
 int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
                 int E, const int64_t* counts, hipStream_t s) {
@@ -980,6 +1365,17 @@ int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K,
              "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
              (long long)M, (long long)K, (long long)N);
   const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length of fwd / dgrad
+  if constexpr (MODE != MODE_WGRAD) {
+    // The persistent kernel needs two k-tiles per output tile, its LDS
+    // (stages, epilogue staging, schedule) and 32-bit offsets for loads that
+    // run up to two k-tiles past the reduction end.
+    if (R > P_BK && schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI <= 160 * 1024 &&
+        (R + 2 * P_BK) * ld * 2 < (int64_t)DM_OOB) {
+      if (R % P_BK)
+        return launch_p64_k<MODE, TB, ET, true>(p0, p1, out, M, K, N, E, counts, s, nblk, tj);
+      return launch_p64_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, tj);
+    }
+  }
   if (MODE != MODE_WGRAD && R % DM_BK)
     return launch_mfma_k<MODE, TB, ET, true>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
   return launch_mfma_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
