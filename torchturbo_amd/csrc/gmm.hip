@@ -642,17 +642,20 @@ constexpr int P_STAGE = 2 * P_OPND;     // A then B
 constexpr int P_EPI = 4096;             // epilogue staging per wave
 
 // K-major 64-deep tile: LDS row r (128 bytes) holds tile row r, its 16-byte
-// chunk c in slot c ^ (r & 7). Fragment for k-step s (0..3): rows
-// r0 + lane % 32, chunk 2 s + lane / 32; further 32-row blocks add 4096.
+// chunk c in slot c ^ ((r >> 1) & 7): any 16 consecutive rows then cover the
+// 16 distinct 16-byte bank groups of a 256-byte bank line, so a fragment
+// read (one chunk of 32 rows per half-wave) is free of bank conflicts.
+// Fragment for k-step s (0..3): rows r0 + lane % 32, chunk 2 s + lane / 32;
+// further 32-row blocks add 4096.
 __device__ __forceinline__ uint32_t fragk64(int r0, int s, int lane) {
   const int r = r0 + (lane & 31);
   const int c = 2 * s + (lane >> 5);
-  return (uint32_t)(r * 128 + ((c ^ (r & 7)) << 4));
+  return (uint32_t)(r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
 }
 
 // Epilogue of the 64-deep kernel: the wave's 128x128 tile in 8 rounds of
 // 32 rows x 64 columns through its private 4 KiB of LDS (row r at 128 r,
-// 16-byte chunk c in slot c ^ (r & 7)), stored as 128-byte row segments with
+// 16-byte chunk c in slot c ^ ((r >> 1) & 7)), stored as 128-byte row segments with
 // buffer stores. The store resource ends at the expert's last row, so
 // stores to rows past it are dropped by the hardware; columns past the
 // output width are given an offset past the resource.
@@ -693,7 +696,8 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
                        : "a"(acc[mi][ni][4 * g]), "a"(acc[mi][ni][4 * g + 1]),
                          "a"(acc[mi][ni][4 * g + 2]), "a"(acc[mi][ni][4 * g + 3]));
           const uint2 v = pack4<ET>(x0, x1, x2, x3);
-          *reinterpret_cast<lds_u32x2*>(region + r_l * 128 + ((c ^ (r_l & 7)) << 4) + 8 * h) =
+          *reinterpret_cast<lds_u32x2*>(region + r_l * 128 + ((c ^ ((r_l >> 1) & 7)) << 4) +
+                                        8 * h) =
               u32x2{v.x, v.y};
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -702,7 +706,7 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = 8 * q + rr;
-        const uint4 v = read_k(region, (uint32_t)(r * 128 + ((ch ^ (r & 7)) << 4)));
+        const uint4 v = read_k(region, (uint32_t)(r * 128 + ((ch ^ ((r >> 1) & 7)) << 4)));
         const uint32_t off = col_ok ? (uint32_t)(32 * mi + r) * row_bytes + (uint32_t)col * 2u
                                     : DM_OOB;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (int)off, 0, 0);
@@ -745,24 +749,26 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   // Loads: every wave brings 8 KiB of A (chunks 0-7) and 8 KiB of B (8-15)
   // per k-tile, 1 KiB per instruction. K-major: rows 64 w + 8 q + lane / 8,
   // slot lane % 8; MN-major: k-rows 16 w + 2 q + lane / 32, slot lane % 32.
-  // Offsets are relative to the tile origin (the resource base); chunk q
-  // adds a uniform q * qstep to the chunk-0 offset.
-  // MN-major: the slot swizzle depends on k-row & 3, which alternates
-  // between even and odd chunks, so odd chunks have a base of their own.
+  // Offsets are relative to the tile origin (the resource base). The slot
+  // swizzle alternates between even and odd chunks q, so each parity has a
+  // base offset of its own and chunk q adds a uniform (q / 2) * qstep.
   uint32_t vbase[2], vodd[2], qstep[2], kstep[2];
-  int kof = 0;
+  int kof = 0, kof_odd = 0;
 #pragma unroll
   for (int op = 0; op < 2; ++op) {
     const bool kmaj = op == 0 ? Lay::A_K : Lay::B_K;
     const int64_t ld = op == 0 ? lda : ldb;
     if (kmaj) {
+      // Row 64 w + 8 q + lane / 8: (row >> 1) & 7 = lane / 16 + 4 (q & 1).
       const int r = 64 * wave + (lane >> 3);
-      const int c = (lane & 7) ^ ((lane >> 3) & 7);
+      const int c = (lane & 7) ^ (lane >> 4);
+      const int c1 = c ^ 4;
       vbase[op] = (uint32_t)(((int64_t)r * ld + 8 * c) * 2);
-      vodd[op] = vbase[op];
-      qstep[op] = (uint32_t)(8 * ld * 2);
+      vodd[op] = (uint32_t)(((int64_t)(r + 8) * ld + 8 * c1) * 2);
+      qstep[op] = (uint32_t)(16 * ld * 2);  // per pair of chunks
       kstep[op] = P_BK * 2;
       kof = 8 * c;
+      kof_odd = 8 * c1;
     } else {
       const int kr = 16 * wave + (lane >> 5);
       const int c = (lane & 31) ^ (4 * (kr & 3));
@@ -799,12 +805,11 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     const int op = is_a ? 0 : 1;
     const bool kmaj = is_a ? Lay::A_K : Lay::B_K;
     const int qq = q & 7;
-    uint32_t vb = (!kmaj && (qq & 1)) ? vodd[op] : vbase[op];
+    uint32_t vb = (qq & 1) ? vodd[op] : vbase[op];
     asm volatile("" : "+v"(vb));  // one register per base, not one per chunk
-    const uint32_t qi = kmaj ? (uint32_t)qq : (uint32_t)(qq >> 1);
-    uint32_t off = vb + (qi * qstep[op] + (uint32_t)k * kstep[op]);
+    uint32_t off = vb + ((uint32_t)(qq >> 1) * qstep[op] + (uint32_t)k * kstep[op]);
     if constexpr (KMASK) {
-      if (kmaj && k * P_BK + kof >= kvalid) off = DM_OOB;
+      if (kmaj && k * P_BK + ((qq & 1) ? kof_odd : kof) >= kvalid) off = DM_OOB;
     }
     const i32x4 rs = is_a ? (nxt ? ra_nxt : ra_cur) : (nxt ? rb_nxt : rb_cur);
     dma16(off, rs, lds_addr_of(stg) + (is_a ? 0u : (uint32_t)P_OPND) +
