@@ -856,17 +856,22 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   auto stage = [&](int g) { return lds + (g & 1) * P_STAGE; };
   uint4 a0[FM], b0[FN], a1[FM], b1[FN];
 
-  // One k-tile: k-steps 0-2 multiply while reading the next k-step; then
-  // wait for k-tile kt + 1 (the only load in flight), barrier (every wave is
-  // past its reads of this stage), and k-step 3 multiplies while reading
-  // k-step 0 of k-tile kt + 1 and loading k-tile kt + 2 into this stage.
+  // One k-tile: k-steps 0-2 multiply while reading the next k-step (and
+  // k-steps 0 and 1 load the B half of k-tile kt + 1 into the other stage,
+  // one load every fourth MFMA slot); then wait for k-tile kt + 1 (the only
+  // loads in flight), barrier (every wave is past its reads of this stage),
+  // and k-step 3 multiplies while reading k-step 0 of k-tile kt + 1 and
+  // loading the A half of k-tile kt + 2 into this stage (every other slot).
+  // Issuing a k-tile's 16 loads in one k-step backs up the vector memory
+  // path and stalls the MFMAs behind it.
   auto step = [&](int kt, int g, auto last_c) {
     constexpr bool LAST = decltype(last_c)::value;
     lds_char* const cur = stage(g);
     lds_char* const nxt = stage(g + 1);
-    const int k2 = kt + 2;
-    const bool to_next = k2 >= nkt;
-    const int kr = to_next ? k2 - nkt : k2;
+    const int k1 = kt + 1, k2 = kt + 2;
+    const bool to_next1 = k1 >= nkt, to_next2 = k2 >= nkt;
+    const int kr1 = to_next1 ? k1 - nkt : k1;
+    const int kr2 = to_next2 ? k2 - nkt : k2;
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       refresh(s + 1);
@@ -876,6 +881,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
         if (i < FM + FN) {
           if (s & 1) frag(cur, s + 1, i, a0, b0); else frag(cur, s + 1, i, a1, b1);
         }
+        if (s <= 1 && (i & 3) == 1) issue_one(nxt, kr1, to_next1, 8 + 4 * s + (i >> 2));
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -886,16 +892,18 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     for (int i = 0; i < FM * FN; ++i) {
       mfma(i, a1, b1);
       if (!LAST && i < FM + FN) frag(nxt, 0, i, a0, b0);
-      issue_one(cur, kr, to_next, i);
+      if (i & 1) issue_one(cur, kr2, to_next2, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
+  // k-tile 0 whole and the A half of k-tile 1 (its B half goes out in the
+  // first step).
 #pragma unroll
   for (int q = 0; q < 16; ++q) issue_one(stage(0), 0, false, q);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) issue_one(stage(1), 1, false, q);
-  TT_WAIT_VMCNT(16);
+  for (int q = 0; q < 8; ++q) issue_one(stage(1), 1, false, q);
+  TT_WAIT_VMCNT(8);
   __builtin_amdgcn_s_barrier();
   refresh(0);
 #pragma unroll
