@@ -167,10 +167,32 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
     // long reductions of heavily loaded experts start early.
     __shared__ int lpt_expert;
     const int lb = blockIdx.x;
-    const int rank = lb / (tiles_i * tiles_j);
-    const int rem = lb % (tiles_i * tiles_j);
-    it = rem / tiles_j;
-    jt = rem % tiles_j;
+    const int per = tiles_i * tiles_j;
+    const int rank = lb / per;
+    const int rem = lb % per;
+    // Block b runs on XCD b % 8. When an expert's tile grid splits into 8
+    // equal rectangles (a x c of them), XCD x takes rectangle x: its blocks
+    // then share a few activation panels in that XCD's L2 (a rectangle of
+    // h x w tiles reads h + w panels), while a heavily loaded expert still
+    // spreads over all XCDs. Otherwise tiles go in row order.
+    int h = 0, w = 0, c = 0;
+    if (per % 8 == 0) {
+      int best = 1 << 30;
+      for (int a = 1; a <= 8; a <<= 1) {
+        const int cc = 8 / a;
+        if (tiles_i % a || tiles_j % cc) continue;
+        const int hh = tiles_i / a, ww = tiles_j / cc;
+        if (hh + ww < best) { best = hh + ww; h = hh; w = ww; c = cc; }
+      }
+    }
+    if (h > 0) {
+      const int x = rem % 8, j = rem / 8;
+      it = (x / c) * h + j / w;
+      jt = (x % c) * w + j % w;
+    } else {
+      it = rem / tiles_j;
+      jt = rem % tiles_j;
+    }
     if (rank >= E) return false;
     // Rank of every expert, its comparisons split over NT / E threads per
     // expert and summed with LDS atomics; int32 counts after the schedule.
