@@ -145,56 +145,78 @@ __global__ __launch_bounds__(256) void unpermute_small_kernel(
   typedef typename TT::storage St;
   constexpr int PR = (PD == kNoProbs || PD == XD) ? XD : TT_F32;
   const int64_t t = blockIdx.x;
-  int rs[KMAX];
-  float ws[KMAX];
+  int rs[KMAX], es[KMAX];
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) {
     rs[j] = 0x7fffffff;
-    ws[j] = 1.0f;
+    es[j] = -1;
     if (j < K) {
       const int r = rows[t * K + j];
       rs[j] = (r >= 0 && r < M) ? r : 0x7fffffff;
       if constexpr (PD != kNoProbs) {
         const int64_t e = experts[t * K + j];
-        ws[j] = (e >= 0 && e < E) ? load_w<PD>(probs, t * E + e) : 1.0f;
+        es[j] = (e >= 0 && e < E) ? (int)e : -1;
       }
     }
   }
-  // Insertion sort by row (K <= KMAX <= 8), carrying the weights.
+  // Insertion sort by row (K <= KMAX <= 8), carrying the expert ids; the
+  // weights are gathered after the sort, alongside the rows, so the row
+  // loads do not wait for them.
 #pragma unroll
   for (int a = 1; a < KMAX; ++a)
 #pragma unroll
     for (int b = a; b > 0; --b) {
       const bool sw = rs[b - 1] > rs[b];
       const int r0 = rs[b - 1], r1 = rs[b];
-      const float w0 = ws[b - 1], w1 = ws[b];
+      const int e0 = es[b - 1], e1 = es[b];
       rs[b - 1] = sw ? r1 : r0;
       rs[b] = sw ? r0 : r1;
-      ws[b - 1] = sw ? w1 : w0;
-      ws[b] = sw ? w0 : w1;
+      es[b - 1] = sw ? e1 : e0;
+      es[b] = sw ? e0 : e1;
     }
+  // Weights also loaded unconditionally (a token's own row of probs, column
+  // 0 for an invalid expert) so that the loads are not serialized.
+  float ws[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    ws[j] = 1.0f;
+    if constexpr (PD != kNoProbs) {
+      const float w = load_w<PD>(probs, t * E + (es[j] >= 0 ? es[j] : 0));
+      ws[j] = es[j] >= 0 ? w : 1.0f;
+    }
+  }
   const int64_t nv = H / V;
+  if (M == 0) {  // no rows: every term is zero
+    St y[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) y[i] = TT::from_f32(0.0f);
+    for (int64_t v = threadIdx.x; v < nv; v += blockDim.x)
+      __builtin_memcpy(out + t * H + v * V, y, sizeof(y));
+    return;
+  }
+  // Rows are loaded unconditionally (an invalid row reads row 0 and counts
+  // as zero): a load under a per-row branch would be waited for before the
+  // next one is issued.
   for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
     St x[KMAX][V];
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
-      if (rs[j] != 0x7fffffff) {
-        __builtin_memcpy(x[j], packed + (int64_t)rs[j] * H + v * V, sizeof(x[j]));
-      } else {
-#pragma unroll
-        for (int i = 0; i < V; ++i) x[j][i] = TT::from_f32(0.0f);
-      }
+      const int64_t r = rs[j] != 0x7fffffff ? rs[j] : 0;
+      __builtin_memcpy(x[j], packed + r * H + v * V, sizeof(x[j]));
     }
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j)
+    for (int j = 0; j < KMAX; ++j) {
+      const bool ok = rs[j] != 0x7fffffff;
 #pragma unroll
       for (int i = 0; i < V; ++i) {
-        if constexpr (PD != kNoProbs) acc[i] += rnd_dt<PR>(TT::to_f32(x[j][i]) * ws[j]);
-        else acc[i] += TT::to_f32(x[j][i]);
+        const float xv = ok ? TT::to_f32(x[j][i]) : 0.0f;
+        if constexpr (PD != kNoProbs) acc[i] += rnd_dt<PR>(xv * ws[j]);
+        else acc[i] += xv;
       }
+    }
     St y[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) y[i] = TT::from_f32(rnd_dt<PR>(acc[i]));
