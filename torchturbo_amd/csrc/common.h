@@ -97,6 +97,33 @@ static inline int tt_elem_size(int dtype) {
 // ---------------------------------------------------------------------------
 // Wave-level primitives.
 // ---------------------------------------------------------------------------
+// Streaming accesses of NB bytes (2, 4, 8 or 16) with the nontemporal hint,
+// for data that a kernel touches exactly once.
+template <int NB>
+struct StreamVec;
+template <>
+struct StreamVec<16> { typedef __attribute__((ext_vector_type(4))) unsigned type; };
+template <>
+struct StreamVec<8> { typedef __attribute__((ext_vector_type(2))) unsigned type; };
+template <>
+struct StreamVec<4> { typedef unsigned type; };
+template <>
+struct StreamVec<2> { typedef unsigned short type; };
+
+template <int NB>
+__device__ __forceinline__ void load_stream(void* dst, const void* src) {
+  typedef typename StreamVec<NB>::type V;
+  const V v = __builtin_nontemporal_load(reinterpret_cast<const V*>(src));
+  __builtin_memcpy(dst, &v, NB);
+}
+template <int NB>
+__device__ __forceinline__ void store_stream(void* dst, const void* src) {
+  typedef typename StreamVec<NB>::type V;
+  V v;
+  __builtin_memcpy(&v, src, NB);
+  __builtin_nontemporal_store(v, reinterpret_cast<V*>(dst));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, TT_WAVE);

@@ -196,13 +196,13 @@ __global__ __launch_bounds__(256) void unpermute_small_kernel(
   }
   // Rows are loaded unconditionally (an invalid row reads row 0 and counts
   // as zero): a load under a per-row branch would be waited for before the
-  // next one is issued.
+  // next one is issued. Each packed row is read once: streaming loads.
   for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
     St x[KMAX][V];
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
       const int64_t r = rs[j] != 0x7fffffff ? rs[j] : 0;
-      __builtin_memcpy(x[j], packed + r * H + v * V, sizeof(x[j]));
+      load_stream<sizeof(x[j])>(x[j], packed + r * H + v * V);
     }
     float acc[V];
 #pragma unroll
