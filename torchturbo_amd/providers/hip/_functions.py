@@ -77,10 +77,15 @@ class TopKRouting(torch.autograd.Function):
         ctx.save_for_backward(logits, top)
         ctx.cfg = (topk, L.TT_SCORE[score_function], int(bool(pre_softmax)), float(scaling_factor or 0.0))
         ctx.mark_non_differentiable(rmap, top)
+        # The routing map and indices get no gradient: do not let autograd
+        # fill zero tensors for them before every backward.
+        ctx.set_materialize_grads(False)
         return probs, rmap, top
 
     @staticmethod
     def backward(ctx, grad_probs, _g_map, _g_top):
+        if grad_probs is None:
+            return None, None, None, None, None, None, None, None, None
         logits, top = ctx.saved_tensors
         topk, sf, pre, scale = ctx.cfg
         T, E = logits.shape
@@ -119,6 +124,7 @@ def route_index(expert_indices: torch.Tensor, num_experts: int, probs: torch.Ten
 class Permute(torch.autograd.Function):
     @staticmethod
     def forward(ctx, tokens, probs, expert_indices, num_experts):
+        ctx.set_materialize_grads(False)  # no zero-filled gradients for rows / counts
         tokens = tokens.contiguous()
         T, H = tokens.shape
         K = expert_indices.shape[1] if expert_indices.dim() == 2 else 0
