@@ -46,6 +46,7 @@
 // the tiles of a heavily loaded expert spread over all XCDs.
 #include "common.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace {
@@ -662,6 +663,9 @@ constexpr int P_BK = 64;
 constexpr int P_OPND = 256 * P_BK * 2;  // one operand tile (32 KiB)
 constexpr int P_STAGE = 2 * P_OPND;     // A then B
 constexpr int P_EPI = 4096;             // epilogue staging per wave
+// wgrad takes the persistent kernel when the mean rows per expert are at most
+// this (a handful of 64-deep k-tiles per output tile).
+constexpr int64_t P_WGRAD_ROWS = 512;
 
 // K-major 64-deep tile: LDS row r (128 bytes) holds tile row r, its 16-byte
 // chunk c in slot c ^ ((r >> 1) & 7): any 16 consecutive rows then cover the
@@ -737,36 +741,166 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
     }
 }
 
+// Weight-gradient work queues of the persistent kernel. A launch owns one
+// slot (slots rotate between launches); the slot holds one ticket counter per
+// tile class (the blocks of one XCD), zeroed by wgrad_queue_reset_kernel on
+// the launch stream just before the launch. Blocks take tickets with atomic
+// adds and leave once a ticket passes the end of their class's list; no block
+// ever waits for another.
+constexpr int WQ_SLOTS = 64, WQ_CLASSES = 8, WQ_STRIDE = 16;
+__device__ int g_wgrad_queue[WQ_SLOTS * WQ_STRIDE];
+
+__global__ void wgrad_queue_reset_kernel(int slot) {
+  if (threadIdx.x < WQ_STRIDE) g_wgrad_queue[slot * WQ_STRIDE + threadIdx.x] = 0;
+}
+
+// Expert ranks, longest first (ties by id): ranked[r] = expert of rank r.
+// cnt and rnk are E ints of scratch each.
+template <int NT>
+__device__ void rank_experts(const int64_t* row_start, int E, int* cnt, int* rnk, int* ranked) {
+  for (int x = threadIdx.x; x < E; x += NT) {
+    cnt[x] = (int)(row_start[x + 1] - row_start[x]);
+    rnk[x] = 0;
+  }
+  __syncthreads();
+  const int parts = E >= NT ? 1 : NT / E;
+  for (int idx = threadIdx.x; idx < E * parts; idx += NT) {
+    const int x = idx % E, part = idx / E;
+    const int y0 = part * E / parts, y1 = (part + 1) * E / parts;
+    const int cx = cnt[x];
+    int r = 0;
+    for (int y = y0; y < y1; ++y) {
+      const int cy = cnt[y];
+      r += (cy > cx) | ((cy == cx) & (y < x));
+    }
+    atomicAdd(&rnk[x], r);
+  }
+  __syncthreads();
+  for (int x = threadIdx.x; x < E; x += NT) ranked[rnk[x]] = x;
+  __syncthreads();
+}
+
+// An expert's wgrad tile grid (tiles_i x tiles_j) split into 8 equal
+// rectangles (a x c of them, h x w tiles each) when it can be: tile rem then
+// lies in rectangle rem % 8, so the tiles of one class (rem = x + 8 j) share
+// h + w activation panels. Otherwise tiles go in row order.
+struct WgradRect {
+  int h, w, c;
+};
+__device__ __forceinline__ WgradRect wgrad_rect(int tiles_i, int tiles_j) {
+  WgradRect r{0, 0, 0};
+  if ((tiles_i * tiles_j) % 8 == 0) {
+    int best = 1 << 30;
+    for (int a = 1; a <= 8; a <<= 1) {
+      const int cc = 8 / a;
+      if (tiles_i % a || tiles_j % cc) continue;
+      const int hh = tiles_i / a, ww = tiles_j / cc;
+      if (hh + ww < best) { best = hh + ww; r.h = hh; r.w = ww; r.c = cc; }
+    }
+  }
+  return r;
+}
+
+// Tile of ticket q in class cls (cx tiles per expert): expert of rank q / cx,
+// its tile rem = cls + nx * (q % cx). Returns the tile's k-tile count (at
+// least two: the pipeline prefetches two k-tiles ahead; an expert without rows
+// runs two k-tiles of zeros and stores a zero gradient).
+template <bool TRANS_B>
+__device__ __forceinline__ int wgrad_tile_at(int q, int cls, int nx, int cx, const WgradRect& rc,
+                                             int tiles_j, const char* p0, const char* p1,
+                                             char* out, int64_t K, int64_t N,
+                                             const int64_t* row_start, const int* ranked,
+                                             TileDesc& t) {
+  const int e = __builtin_amdgcn_readfirstlane(ranked[q / cx]);
+  const int rem = cls + nx * (q % cx);
+  int it, jt;
+  if (rc.h > 0) {
+    const int x = rem % 8, j = rem / 8;
+    it = (x / rc.c) * rc.h + j / rc.w;
+    jt = (x % rc.c) * rc.w + j % rc.w;
+  } else {
+    it = rem / tiles_j;
+    jt = rem % tiles_j;
+  }
+  t.e = e;
+  t.seg0 = rfl64(row_start[e]);
+  t.nrows = rfl64(row_start[e + 1]) - t.seg0;
+  t.R = t.nrows;
+  if constexpr (!TRANS_B) {
+    t.a = p0 + t.seg0 * K * 2; t.lda = K;  // x
+    t.b = p1 + t.seg0 * N * 2; t.ldb = N;  // dy
+    t.I = K; t.J = N;
+  } else {
+    t.a = p1 + t.seg0 * N * 2; t.lda = N;  // dy
+    t.b = p0 + t.seg0 * K * 2; t.ldb = K;  // x
+    t.I = N; t.J = K;
+  }
+  t.c = out + (int64_t)e * K * N * 2; t.ldc = t.J;
+  t.i0 = (int64_t)it * DM_BM;
+  t.j0 = (int64_t)jt * DM_BN;
+  const int nkt = (int)((t.R + P_BK - 1) / P_BK);
+  return nkt > 2 ? nkt : 2;
+}
+
 template <int MODE, bool TRANS_B, int ET, bool KMASK>
 __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__ p0,
                                                         const char* __restrict__ p1,
                                                         char* __restrict__ out, int64_t M,
                                                         int64_t K, int64_t N, int E,
                                                         const int64_t* __restrict__ counts,
-                                                        int tiles_j) {
-  static_assert(MODE != MODE_WGRAD, "fwd / dgrad only");
+                                                        int tiles_i, int tiles_j, int qslot) {
+  constexpr bool WG = MODE == MODE_WGRAD;
+  static_assert(!(WG && KMASK), "wgrad reduces over rows (no K-major tail)");
   typedef Layout<MODE, TRANS_B> Lay;
   constexpr int WT = 128, FM = 4, FN = 4;
   __shared__ __align__(16) char lds_raw[2 * P_STAGE];
   __shared__ __align__(16) char epi_raw[4 * P_EPI];
+  __shared__ int ticket_slot[2];
   extern __shared__ __align__(16) char smem[];  // expert schedule
   int64_t* row_start = reinterpret_cast<int64_t*>(smem);
   int* tile_start = reinterpret_cast<int*>(row_start + E + 1);
   scan_counts<DM_NT>(counts, E, DM_BM, row_start, tile_start);
 
   const int G = gridDim.x;
-  const int pos = xcd_remap(blockIdx.x, G);
-  const int total = tile_start[E] * tiles_j;
-  if (pos >= total) return;
-  const int ntiles = (total - pos + G - 1) / G;
-  const int64_t R = MODE == MODE_FWD ? K : N;
-  const int nkt = (int)((R + P_BK - 1) / P_BK);  // >= 2 (host check)
+  // fwd / dgrad: block position pos walks tiles pos, pos + G, ... (XCD-grouped
+  // positions). wgrad: class cls = blockIdx % nx takes tickets from its queue.
+  int pos = 0, ntiles = 0, total = 0;
+  int nx = 1, cls = 0, cx = 1;
+  int* queue = nullptr;
+  int* ranked = nullptr;
+  WgradRect rect{0, 0, 0};
+  int q0 = 0;
+  if constexpr (!WG) {
+    pos = xcd_remap(blockIdx.x, G);
+    total = tile_start[E] * tiles_j;
+    if (pos >= total) return;
+    ntiles = (total - pos + G - 1) / G;
+  } else {
+    int* cnt = tile_start + E + 1;
+    ranked = cnt + 2 * E;
+    rank_experts<DM_NT>(row_start, E, cnt, cnt + E, ranked);
+    nx = G >= WQ_CLASSES ? WQ_CLASSES : 1;
+    cls = blockIdx.x % nx;
+    const int per = tiles_i * tiles_j;
+    cx = (per - cls + nx - 1) / nx;
+    total = E * cx;
+    if (cx == 0) return;
+    rect = wgrad_rect(tiles_i, tiles_j);
+    queue = g_wgrad_queue + qslot * WQ_STRIDE + cls;
+    if (threadIdx.x == 0) ticket_slot[0] = atomicAdd(queue, 1);
+    __syncthreads();
+    q0 = ticket_slot[0];
+    if (q0 >= total) return;
+  }
+  const int64_t R = MODE == MODE_FWD ? K : N;  // fwd / dgrad reduction length
+  int nkt_c = (int)((R + P_BK - 1) / P_BK);     // >= 2 (host check)
+  int nkt_n = nkt_c;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t lda = MODE == MODE_FWD ? K : N;
-  const int64_t ldb = TRANS_B ? K : N;
+  const int64_t lda = WG ? (TRANS_B ? N : K) : (MODE == MODE_FWD ? K : N);
+  const int64_t ldb = WG ? (TRANS_B ? K : N) : (TRANS_B ? K : N);
 
   // Loads: every wave brings 8 KiB of A (chunks 0-7) and 8 KiB of B (8-15)
   // per k-tile, 1 KiB per instruction. K-major: rows 64 w + 8 q + lane / 8,
@@ -802,24 +936,46 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     }
   }
 
+  // Resources based at the tile origin. fwd / dgrad: A is K-major (the
+  // expert's rows), B the expert's weights. wgrad: both operands are
+  // MN-major over the expert's rows, so reduction rows past the expert's
+  // end read as zeros.
   auto rsrc_a = [&](const TileDesc& t, bool valid) -> i32x4 {
     if (!valid) return make_rsrc(p0, 0);
-    const int64_t toff = t.i0 * t.lda * 2;  // A is K-major in fwd / dgrad
+    if constexpr (WG) return make_rsrc(t.a + t.i0 * 2, t.R * t.lda * 2 - t.i0 * 2);
+    const int64_t toff = t.i0 * t.lda * 2;
     return make_rsrc(t.a + toff, t.nrows * t.lda * 2 - toff);
   };
   auto rsrc_b = [&](const TileDesc& t, bool valid) -> i32x4 {
     if (!valid) return make_rsrc(p0, 0);
+    if constexpr (WG) return make_rsrc(t.b + t.j0 * 2, t.R * t.ldb * 2 - t.j0 * 2);
     const int64_t toff = Lay::B_K ? t.j0 * t.ldb * 2 : t.j0 * 2;
     return make_rsrc(t.b + toff, K * N * 2 - toff);
   };
 
+  // wgrad claims the next tile's ticket two or three k-tiles before the end
+  // of the current one (late enough to keep the assignment greedy, early
+  // enough to prefetch the next tile's first k-tiles): the ticket is taken at
+  // k-tile claim_kt, published at k-tile nkt_c - 2 and decoded right after
+  // that k-tile's barrier, before its loads of the next tile.
   TileDesc tc, tn;
-  tile_at<MODE, TRANS_B, 2>(pos, p0, p1, out, K, N, E, tiles_j, row_start, tile_start, tc);
-  if (ntiles > 1)
-    tile_at<MODE, TRANS_B, 2>(pos + G, p0, p1, out, K, N, E, tiles_j, row_start, tile_start, tn);
+  bool has_next;
+  if constexpr (WG) {
+    nkt_c = wgrad_tile_at<TRANS_B>(q0, cls, nx, cx, rect, tiles_j, p0, p1, out, K, N, row_start,
+                                   ranked, tc);
+    has_next = false;  // known at k-tile nkt_c - 2
+  } else {
+    tile_at<MODE, TRANS_B, 2>(pos, p0, p1, out, K, N, E, tiles_j, row_start, tile_start, tc);
+    has_next = ntiles > 1;
+    if (has_next)
+      tile_at<MODE, TRANS_B, 2>(pos + G, p0, p1, out, K, N, E, tiles_j, row_start, tile_start,
+                                tn);
+  }
   i32x4 ra_cur = rsrc_a(tc, true), rb_cur = rsrc_b(tc, true);
-  i32x4 ra_nxt = rsrc_a(tn, ntiles > 1), rb_nxt = rsrc_b(tn, ntiles > 1);
+  i32x4 ra_nxt = rsrc_a(tn, has_next), rb_nxt = rsrc_b(tn, has_next);
   const int kvalid = (int)R;
+  int pending = 0;  // wgrad: ticket of the next tile (thread 0)
+  int n = 0;        // tiles finished
 
   // Chunk q (0-7 A, 8-15 B) of k-tile k of the current or next tile.
   auto issue_one = [&](lds_char* stg, int k, bool nxt, int q) {
@@ -891,9 +1047,13 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     lds_char* const cur = stage(g);
     lds_char* const nxt = stage(g + 1);
     const int k1 = kt + 1, k2 = kt + 2;
-    const bool to_next1 = k1 >= nkt, to_next2 = k2 >= nkt;
-    const int kr1 = to_next1 ? k1 - nkt : k1;
-    const int kr2 = to_next2 ? k2 - nkt : k2;
+    const bool to_next1 = k1 >= nkt_c, to_next2 = k2 >= nkt_c;
+    const int kr1 = to_next1 ? k1 - nkt_c : k1;
+    const int kr2 = to_next2 ? k2 - nkt_c : k2;
+    if constexpr (WG) {
+      const int claim_kt = nkt_c > 3 ? nkt_c - 3 : 0;
+      if (kt == claim_kt && threadIdx.x == 0) pending = atomicAdd(queue, 1);
+    }
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       refresh(s + 1);
@@ -908,7 +1068,24 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       }
     }
     TT_WAIT_VMCNT(0);
+    if constexpr (WG) {
+      // The claimed ticket has returned (the wait above covers it); the
+      // barrier publishes it, and the next tile is decoded before this
+      // k-tile's loads of it.
+      if (kt == nkt_c - 2 && threadIdx.x == 0) ticket_slot[n & 1] = pending;
+    }
     TT_LDS_BARRIER();
+    if constexpr (WG) {
+      if (kt == nkt_c - 2) {
+        const int q = ticket_slot[n & 1];
+        has_next = q < total;
+        if (has_next)
+          nkt_n = wgrad_tile_at<TRANS_B>(q, cls, nx, cx, rect, tiles_j, p0, p1, out, K, N,
+                                         row_start, ranked, tn);
+        ra_nxt = rsrc_a(tn, has_next);
+        rb_nxt = rsrc_b(tn, has_next);
+      }
+    }
     refresh(0);
 #pragma unroll
     for (int i = 0; i < FM * FN; ++i) {
@@ -933,28 +1110,36 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
 
   lds_char* const epi = (lds_char*)epi_raw + wave * P_EPI;
   int g = 0;
-  for (int n = 0;;) {
+  for (;;) {
 #pragma unroll
     for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
       for (int ni = 0; ni < FN; ++ni)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
-    for (int kt = 0; kt < nkt - 1; ++kt, ++g) step(kt, g, std::false_type{});
-    step(nkt - 1, g, std::true_type{});
+    for (int kt = 0; kt < nkt_c - 1; ++kt, ++g) step(kt, g, std::false_type{});
+    step(nkt_c - 1, g, std::true_type{});
     ++g;
     __builtin_amdgcn_sched_barrier(0);
     store_wave_tile_p64<ET>(acc, tc, tc.i0 + wm * WT, tc.j0 + wn * WT, epi);
-    if (++n == ntiles) break;
+    if (!has_next) break;
     tc = tn;
+    nkt_c = nkt_n;
     ra_cur = ra_nxt;
     rb_cur = rb_nxt;
-    const bool more = n + 1 < ntiles;
-    if (more)
-      tile_at<MODE, TRANS_B, 2>(pos + (n + 1) * G, p0, p1, out, K, N, E, tiles_j, row_start,
-                                tile_start, tn);
-    ra_nxt = rsrc_a(tn, more);
-    rb_nxt = rsrc_b(tn, more);
+    if constexpr (!WG) {
+      has_next = n + 2 < ntiles;
+      if (has_next)
+        tile_at<MODE, TRANS_B, 2>(pos + (n + 2) * G, p0, p1, out, K, N, E, tiles_j, row_start,
+                                  tile_start, tn);
+      ra_nxt = rsrc_a(tn, has_next);
+      rb_nxt = rsrc_b(tn, has_next);
+    } else {
+      has_next = false;  // decided during the next tile
+      ra_nxt = rsrc_a(tn, false);
+      rb_nxt = rsrc_b(tn, false);
+    }
+    ++n;
     refresh(0);
 #pragma unroll
     for (int i = 0; i < FM + FN; ++i) frag(stage(g), 0, i, a0, b0);
@@ -1368,18 +1553,31 @@ int cu_count() {
   return cached[dev];
 }
 
+// Dynamic LDS of the persistent kernel: the expert schedule plus the expert
+// ranking of wgrad.
+size_t p64_schedule_bytes(int E) { return schedule_bytes(E) + (size_t)E * sizeof(int); }
+
 template <int MODE, bool TB, int ET, bool KMASK>
 int launch_p64_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
-                 int E, const int64_t* counts, hipStream_t s, int64_t nblk, int tj) {
-  const size_t lds = schedule_bytes(E);  // stages and epilogue staging are static LDS
+                 int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj) {
+  const size_t lds = p64_schedule_bytes(E);  // stages and epilogue staging are static LDS
   static size_t allowed = 64 * 1024;
   const int rc = allow_lds(&gmm_p64_kernel<MODE, TB, ET, KMASK>, lds, allowed);
   if (rc != TT_OK) return rc;
+  int slot = 0;
+  if constexpr (MODE == MODE_WGRAD) {
+    // A queue slot of its own for this launch, zeroed on the launch stream.
+    static std::atomic<unsigned> next_slot{0};
+    slot = (int)(next_slot.fetch_add(1, std::memory_order_relaxed) % WQ_SLOTS);
+    hipLaunchKernelGGL(wgrad_queue_reset_kernel, dim3(1), dim3(64), 0, s, slot);
+    const int rq = tt_check_launch("gmm");
+    if (rq != TT_OK) return rq;
+  }
   const int64_t cus = cu_count();
   const int64_t grid = nblk < cus ? nblk : cus;
   hipLaunchKernelGGL((gmm_p64_kernel<MODE, TB, ET, KMASK>), dim3((unsigned)grid), dim3(DM_NT),
                      lds, s, static_cast<const char*>(p0), static_cast<const char*>(p1),
-                     static_cast<char*>(out), M, K, N, E, counts, tj);
+                     static_cast<char*>(out), M, K, N, E, counts, ti, tj, slot);
   return tt_check_launch("gmm");
 }
 
@@ -1400,16 +1598,26 @@ int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K,
              "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
              (long long)M, (long long)K, (long long)N);
   const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length of fwd / dgrad
+  const bool p64_lds = p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI <= 160 * 1024;
   if constexpr (MODE != MODE_WGRAD) {
     // The persistent kernel needs two k-tiles per output tile, its LDS
     // (stages, epilogue staging, schedule) and 32-bit offsets for loads that
     // run up to two k-tiles past the reduction end.
-    if (R > P_BK && schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI <= 160 * 1024 &&
-        (R + 2 * P_BK) * ld * 2 < (int64_t)DM_OOB) {
+    if (R > P_BK && p64_lds && (R + 2 * P_BK) * ld * 2 < (int64_t)DM_OOB) {
       if (R % P_BK)
-        return launch_p64_k<MODE, TB, ET, true>(p0, p1, out, M, K, N, E, counts, s, nblk, tj);
-      return launch_p64_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, tj);
+        return launch_p64_k<MODE, TB, ET, true>(p0, p1, out, M, K, N, E, counts, s, nblk, ti,
+                                                tj);
+      return launch_p64_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, ti,
+                                               tj);
     }
+  } else {
+    // Short reductions (few rows per expert on average, known without the
+    // counts): the persistent kernel, whose epilogue stores overlap the next
+    // tile's loads. Long ones stream faster through the four-stage kernel.
+    // wgrad reduces over each expert's rows (at most M; the loads run up to
+    // two k-tiles past an expert's end).
+    if (M <= (int64_t)E * P_WGRAD_ROWS && p64_lds && (M + 2 * P_BK) * ld * 2 < (int64_t)DM_OOB)
+      return launch_p64_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
   }
   if (MODE != MODE_WGRAD && R % DM_BK)
     return launch_mfma_k<MODE, TB, ET, true>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
