@@ -21,9 +21,14 @@
 //   gfx950 transposing load ds_read_b64_tr_b16 (no register transpose).
 //   MFMAs, fragment reads of the next k-step and DMA issue are interleaved
 //   one per slot. The epilogue converts to 16 bits in hardware and stores
-//   through LDS as full 256-byte rows. Serves wgrad and short reductions.
-// * gmm_p64_kernel (bf16/f16 fwd/dgrad with a reduction longer than 64):
-//   persistent, one block per CU walking a strided list of output tiles;
+//   through LDS as full 256-byte rows. Serves wgrad with long expert
+//   reductions (its three k-tiles in flight stream two activation operands
+//   fastest) and short fwd/dgrad reductions.
+// * gmm_p64_kernel (bf16/f16 fwd/dgrad with a reduction longer than 64, and
+//   wgrad with few rows per expert): persistent, one block per CU; fwd/dgrad
+//   blocks walk a strided list of output tiles, wgrad blocks take tickets
+//   from per-XCD queues over the experts' tiles, longest expert first, and
+//   claim the next ticket two or three k-tiles before the current tile ends.
 //   256x256x64 tiles through two 64 KiB LDS stages, so K-major rows are
 //   whole 128-byte lines. The k-tiles of consecutive tiles form one stream
 //   (the next tile's first loads overlap the current tile's last k-tile and
