@@ -402,7 +402,8 @@ def test_grouped_matmul_integer_exact(hip_ops):
 # ---------------------------------------------------------------------------
 # FP8 block-scaled grouped GEMM
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("counts,K,N", [([0, 130, 7, 256], 256, 384), ([64, 64], 512, 256)])
+@pytest.mark.parametrize("counts,K,N", [([0, 130, 7, 256], 256, 384), ([64, 64], 512, 256),
+                                         ([5, 0, 300, 129], 208, 272), ([128, 1, 90], 96, 640)])
 def test_grouped_matmul_fp8(hip_ops, counts, K, N):
     g = torch.Generator().manual_seed(K + N)
     E, M = len(counts), sum(counts)
@@ -435,3 +436,43 @@ def test_fp8_dequant_exact_through_gemm(hip_ops):
     y = hip_ops.grouped_matmul_fp8(x.to(DEV), q.to(DEV), s.to(DEV), [K] * E)
     expect = torch.cat([deq[e].t() for e in range(E)])  # row k of expert e = W[:, k]
     assert torch.equal(y.cpu(), expect)
+
+
+def test_fp8_dequant_exact_through_dgrad(hip_ops):
+    """dy = identity rows per expert: dx = dy @ W_deq returns the dequantized weight rows
+    bit-exactly (each output is one product with 1.0 plus exact zeros); covers the
+    N-major (transposed) e4m3 operand with partial 512-column tiles and partial
+    scale blocks."""
+    E, N, K = 3, 384, 320
+    g = torch.Generator().manual_seed(2)
+    master = torch.randn(E, N, K, generator=g) * 0.3
+    q, s = o_fp8.quantize_experts(master)
+    deq = o_fp8.dequantize_experts(q, s)
+    x = torch.randn(E * N, K, generator=g).to(torch.bfloat16).to(DEV).requires_grad_()
+    y = hip_ops.grouped_matmul_fp8(x, q.to(DEV), s.to(DEV), [N] * E)
+    y.backward(torch.eye(N).repeat(E, 1).to(torch.bfloat16).to(DEV))
+    assert torch.equal(x.grad.cpu(), deq.reshape(E * N, K))
+
+
+def test_grouped_matmul_fp8_many_tiles(hip_ops):
+    """More output tiles than compute units (each persistent block walks several
+    tiles), skewed loads with empty experts; fp32 reference of the dequantized weights."""
+    E, K, N = 64, 512, 1024
+    g = torch.Generator().manual_seed(5)
+    counts = [int(c) for c in torch.randint(0, 600, (E,), generator=g)]
+    counts[3] = counts[17] = 0
+    M = sum(counts)
+    master = torch.randn(E, N, K, generator=g) * 0.02
+    q, s = o_fp8.quantize_experts(master)
+    deq = o_fp8.dequantize_experts(q, s).to(DEV)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV).requires_grad_()
+    dy = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    y = hip_ops.grouped_matmul_fp8(x, q.to(DEV), s.to(DEV), counts)
+    y.backward(dy)
+    xs = torch.split(x.detach().float(), counts)
+    ds = torch.split(dy.float(), counts)
+    yr = torch.cat([xs[e] @ deq[e].float().t() for e in range(E)])
+    dxr = torch.cat([ds[e] @ deq[e].float() for e in range(E)])
+    for a, b, name in ((y, yr, "y"), (x.grad, dxr, "dx")):
+        mx, mean = rel_errors(a.float().cpu(), b.cpu())
+        assert mx <= 1e-2 and mean <= 2e-3, f"{name}: {mx:.3e} {mean:.3e}"

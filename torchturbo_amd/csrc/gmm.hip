@@ -1426,6 +1426,387 @@ __global__ __launch_bounds__(DM_NT) void gmm_fp8_kernel(const char* __restrict__
 // ---------------------------------------------------------------------------
 // fp32 path (toy shapes and fp32 models): 64x64 tiles, 4x4 outputs per thread.
 // ---------------------------------------------------------------------------
+// ===========================================================================
+// Persistent FP8-weight kernel (fwd / dgrad): e4m3 weights [E, N, K] with
+// 128x128 block scales, bf16 activations, 128x512x64 output tiles. The four
+// waves share the tile's 128 rows and take 128 columns each, so an expert's
+// rows are padded to a multiple of 128 only; per 64-deep k-tile the block
+// loads 16 KiB of activations and 32 KiB of e4m3 weights (the bytes of a
+// 256x256 tile with bf16 A and e4m3 B). The weights stay e4m3 in LDS: each
+// wave reads its own B fragments as e4m3 bytes (plain 8-byte reads of
+// K-major rows in fwd; gfx950 transposing 8-bit reads of N-major rows in
+// dgrad) and dequantises them in registers, bf16(f32(q) * f32(scale)) with
+// the hardware e4m3 -> f32 decode and round-to-nearest-even. A wave's 128
+// columns lie in one 128-column scale block, so it needs one scale per
+// k-tile, read from a private LDS row filled at the tile switch (prefetched
+// into a register one tile ahead). Otherwise the persistent schedule and the
+// two-stage pipeline are those of gmm_p64_kernel.
+// ===========================================================================
+constexpr int Q_BM = 128, Q_BN = 512, Q_BK = 64;
+constexpr int Q_A = Q_BM * Q_BK * 2;  // A tile, bf16 (16 KiB)
+constexpr int Q_B = Q_BN * Q_BK;      // B tile, e4m3 (32 KiB)
+constexpr int Q_STAGE = Q_A + Q_B;
+constexpr int Q_SMAX = 128;           // scale blocks along the reduction
+
+// Output tile L of the 128x512 schedule (slot-major, n-tile minor).
+template <int MODE>
+__device__ __forceinline__ void q8_tile_at(int L, const char* p0, const char* qw, char* out,
+                                           int64_t K, int64_t N, int E, int tiles_j,
+                                           const int64_t* row_start, const int* tile_start,
+                                           TileDesc& t) {
+  const int slot = L / tiles_j, jt = L % tiles_j;
+  int lo = 0, hi = E - 1;  // last e with tile_start[e] <= slot
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tile_start[mid] <= slot) lo = mid; else hi = mid - 1;
+  }
+  const int e = __builtin_amdgcn_readfirstlane(lo);
+  t.e = e;
+  t.seg0 = rfl64(row_start[e]);
+  t.nrows = rfl64(row_start[e + 1]) - t.seg0;
+  const int ts_e = __builtin_amdgcn_readfirstlane(tile_start[e]);
+  t.b = qw + (int64_t)e * N * K;
+  if constexpr (MODE == MODE_FWD) {
+    t.a = p0 + t.seg0 * K * 2; t.lda = K;
+    t.I = t.nrows; t.J = N; t.R = K;
+    t.c = out + t.seg0 * N * 2; t.ldc = N;
+  } else {
+    t.a = p0 + t.seg0 * N * 2; t.lda = N;
+    t.I = t.nrows; t.J = K; t.R = N;
+    t.c = out + t.seg0 * K * 2; t.ldc = K;
+  }
+  t.ldb = K;
+  t.i0 = (int64_t)(slot - ts_e) * Q_BM;
+  t.j0 = (int64_t)jt * Q_BN;
+}
+
+// Eight e4m3 bytes (k order) -> one bf16 B fragment.
+__device__ __forceinline__ uint4 deq8(uint2 q, float s) {
+  const uint2 lo = deq4(q.x, s), hi = deq4(q.y, s);
+  return uint4{lo.x, lo.y, hi.x, hi.y};
+}
+
+template <int MODE, bool KMASK>
+__global__ __launch_bounds__(DM_NT) void gmm_q8_kernel(const char* __restrict__ p0,
+                                                       const char* __restrict__ qw,
+                                                       const char* __restrict__ scale, int sdt,
+                                                       char* __restrict__ out, int64_t M,
+                                                       int64_t K, int64_t N, int E,
+                                                       const int64_t* __restrict__ counts,
+                                                       int tiles_j) {
+  static_assert(MODE != MODE_WGRAD, "weights are the B operand");
+  constexpr int FM = 4, FN = 4;
+  __shared__ __align__(16) char lds_raw[2 * Q_STAGE];
+  __shared__ __align__(16) char epi_raw[4 * P_EPI];
+  __shared__ float sc_raw[4 * Q_SMAX];
+  extern __shared__ __align__(16) char smem[];  // expert schedule
+  int64_t* row_start = reinterpret_cast<int64_t*>(smem);
+  int* tile_start = reinterpret_cast<int*>(row_start + E + 1);
+  scan_counts<DM_NT>(counts, E, Q_BM, row_start, tile_start);
+
+  const int G = gridDim.x;
+  const int pos = xcd_remap(blockIdx.x, G);
+  const int total = tile_start[E] * tiles_j;
+  if (pos >= total) return;
+  const int ntiles = (total - pos + G - 1) / G;
+  const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length
+  const int nkt = (int)((R + Q_BK - 1) / Q_BK);  // >= 2 (host check)
+  const int64_t snb = (N + 127) / 128, skb = (K + 127) / 128;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t lda = MODE == MODE_FWD ? K : N;
+
+  // ---- Loads (offsets relative to the tile origin, the resource base).
+  // A (K-major, 128 rows of 128 bytes per k-tile): chunk q (0-3) of wave w
+  // covers rows 32 w + 8 q + lane / 8, LDS slot lane % 8 holding k-chunk
+  // slot ^ ((row >> 1) & 7); the swizzle alternates with q's parity.
+  // B fwd (K-major e4m3, 512 rows of 64 bytes): chunk q (0-7) of wave w
+  // covers rows 128 w + 16 q + lane / 4, slot lane % 4 holding k-chunk
+  // slot ^ ((row >> 2) & 3) = (lane % 4) ^ (lane / 16 % 4).
+  // B dgrad (N-major e4m3, 64 k-rows of 512 bytes): chunk q of wave w covers
+  // k-rows 16 w + 2 q + lane / 32, slot lane % 32 holding column chunk
+  // slot ^ ((k-row % 8) << 1); the swizzle repeats every four chunks.
+  uint32_t a_even, a_odd, b_base[4];
+  int a_kof_even, a_kof_odd, b_kof = 0;
+  {
+    const int r = 32 * wave + (lane >> 3);
+    const int c = (lane & 7) ^ (lane >> 4);
+    const int c1 = c ^ 4;
+    a_even = (uint32_t)(((int64_t)r * lda + 8 * c) * 2);
+    a_odd = (uint32_t)(((int64_t)(r + 8) * lda + 8 * c1) * 2);
+    a_kof_even = 8 * c;
+    a_kof_odd = 8 * c1;
+  }
+  if constexpr (MODE == MODE_FWD) {
+    const int j = 128 * wave + (lane >> 2);
+    const int c = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) b_base[h] = (uint32_t)((int64_t)j * K + 16 * c);
+    b_kof = 16 * c;
+  } else {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int kr = 16 * wave + 2 * h + (lane >> 5);  // chunk q = 4 q' + h
+      const int c = (lane & 31) ^ ((kr & 7) << 1);
+      b_base[h] = (uint32_t)((int64_t)kr * K + 16 * c);
+    }
+  }
+  const uint32_t a_qstep = (uint32_t)(16 * lda * 2);  // A: per pair of chunks
+  // B: per chunk (fwd, 16 rows) or per four chunks (dgrad, 8 k-rows).
+  const uint32_t b_qstep = MODE == MODE_FWD ? (uint32_t)(16 * K) : (uint32_t)(8 * K);
+  const uint32_t b_kstep = MODE == MODE_FWD ? (uint32_t)Q_BK : (uint32_t)(Q_BK * K);
+
+  auto rsrc_a = [&](const TileDesc& t, bool valid) -> i32x4 {
+    if (!valid) return make_rsrc(p0, 0);
+    const int64_t toff = t.i0 * t.lda * 2;
+    return make_rsrc(t.a + toff, t.nrows * t.lda * 2 - toff);
+  };
+  auto rsrc_b = [&](const TileDesc& t, bool valid) -> i32x4 {
+    if (!valid) return make_rsrc(p0, 0);
+    const int64_t toff = MODE == MODE_FWD ? t.j0 * K : t.j0;
+    return make_rsrc(t.b + toff, N * K - toff);
+  };
+
+  TileDesc tc, tn;
+  q8_tile_at<MODE>(pos, p0, qw, out, K, N, E, tiles_j, row_start, tile_start, tc);
+  bool has_next = ntiles > 1;
+  if (has_next) q8_tile_at<MODE>(pos + G, p0, qw, out, K, N, E, tiles_j, row_start, tile_start, tn);
+  i32x4 ra_cur = rsrc_a(tc, true), rb_cur = rsrc_b(tc, true);
+  i32x4 ra_nxt = rsrc_a(tn, has_next), rb_nxt = rsrc_b(tn, has_next);
+  const int kvalid = (int)R;
+
+  // Scales of this wave's 128-column block along the reduction: fwd,
+  // scale[e][(j0 + 128 w) / 128][kb]; dgrad, scale[e][nb][(j0 + 128 w) / 128].
+  const int nsc = (int)(MODE == MODE_FWD ? skb : snb);
+  auto load_scales = [&](const TileDesc& t, float (&v)[2]) {
+    const int64_t colblk = (t.j0 + 128 * wave) / 128;
+    const int64_t cb = MODE == MODE_FWD ? (colblk < snb ? colblk : snb - 1)
+                                        : (colblk < skb ? colblk : skb - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = lane + 64 * h;
+      v[h] = 1.0f;
+      if (i < nsc) {
+        const int64_t off = (int64_t)t.e * snb * skb +
+                            (MODE == MODE_FWD ? cb * skb + i : (int64_t)i * skb + cb);
+        v[h] = sdt == TT_F32 ? reinterpret_cast<const float*>(scale)[off]
+                             : bf16_to_f32(reinterpret_cast<const uint16_t*>(scale)[off]);
+      }
+    }
+  };
+  float* const sc_w = sc_raw + wave * Q_SMAX;
+  float sv_next[2];
+  {
+    float v[2];
+    load_scales(tc, v);
+    sc_w[lane] = v[0];
+    sc_w[lane + 64] = v[1];
+  }
+  if (has_next) load_scales(tn, sv_next);
+
+  // Chunk q (0-3 A, 4-11 B) of k-tile k of the current or next tile.
+  auto issue_one = [&](lds_char* stg, int k, bool nxt, int q) {
+    uint32_t off, dst;
+    i32x4 rs;
+    if (q < 4) {
+      uint32_t vb = (q & 1) ? a_odd : a_even;
+      asm volatile("" : "+v"(vb));
+      off = vb + ((uint32_t)(q >> 1) * a_qstep + (uint32_t)k * (Q_BK * 2));
+      if constexpr (KMASK) {
+        if (k * Q_BK + ((q & 1) ? a_kof_odd : a_kof_even) >= kvalid) off = DM_OOB;
+      }
+      rs = nxt ? ra_nxt : ra_cur;
+      dst = (uint32_t)(4 * wave + q) * 1024u;
+    } else {
+      const int qb = q - 4;
+      uint32_t vb = MODE == MODE_FWD ? b_base[0] : b_base[qb & 3];
+      asm volatile("" : "+v"(vb));
+      off = vb + ((uint32_t)(MODE == MODE_FWD ? qb : qb >> 2) * b_qstep + (uint32_t)k * b_kstep);
+      if constexpr (KMASK && MODE == MODE_FWD) {
+        if (k * Q_BK + b_kof >= kvalid) off = DM_OOB;
+      }
+      rs = nxt ? rb_nxt : rb_cur;
+      dst = (uint32_t)Q_A + (uint32_t)(8 * wave + qb) * 1024u;
+    }
+    dma16(off, rs, lds_addr_of(stg) + dst);
+  };
+
+  // Fragment offsets. A: rows 32 mi + lane % 32 (fragk64). B fwd: row
+  // 128 w + 32 ni + lane % 32, bytes 16 s + 8 (lane / 32) of its 64, chunk
+  // swizzled by (lane / 4) % 4; ni adds 2048. B dgrad: 16-lane group g,
+  // index i: k-row 16 s + 8 (g / 2) + i / 2, columns 128 w + 32 ni +
+  // 16 (g % 2) + 8 (i % 2); ni adds 64 (two chunks; the row swizzle only
+  // touches chunk bits 1-3, so it commutes with +2 chunks when ni is even,
+  // and the swizzled chunk of block ni is computed per ni below).
+  uint32_t a_k[4], b_f[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    a_k[s] = fragk64(0, s, lane);
+    if constexpr (MODE == MODE_FWD) {
+      const int f = (lane >> 2) & 3;
+      b_f[s] = (uint32_t)Q_A + (uint32_t)(128 * wave + (lane & 31)) * 64u +
+               (uint32_t)((s ^ f) << 4) + 8u * (uint32_t)(lane >> 5);
+    } else {
+      const int g = lane >> 4, i = lane & 15;
+      const int kr = 16 * s + 8 * (g >> 1) + (i >> 1);
+      b_f[s] = (uint32_t)Q_A + (uint32_t)kr * 512u + 8u * (uint32_t)(i & 1);
+    }
+  }
+  // dgrad: physical chunk of column chunk c at k-row kr is c ^ ((kr % 8) << 1);
+  // per fragment (s, ni) the lane's logical chunk is 8 w + 2 ni + g % 2.
+  auto b_off = [&](int s, int ni) -> uint32_t {
+    if constexpr (MODE == MODE_FWD) {
+      return b_f[s] + (uint32_t)ni * 2048u;
+    } else {
+      const int g = lane >> 4, i = lane & 15;
+      const int c = 8 * wave + 2 * ni + (g & 1);
+      const int p = c ^ (((i >> 1) & 7) << 1);
+      return b_f[s] + (uint32_t)p * 16u;
+    }
+  };
+
+  f32x16 acc[FM][FN];
+  uint32_t ao, bo[FN];
+  auto refresh = [&](int s) {
+    ao = a_k[s];
+    asm volatile("" : "+v"(ao));
+#pragma unroll
+    for (int i = 0; i < FN; ++i) bo[i] = b_off(s, i);
+    asm volatile("" : "+v"(bo[0]), "+v"(bo[1]), "+v"(bo[2]), "+v"(bo[3]));
+  };
+  auto read_b8 = [&](lds_char* stg, uint32_t off) -> uint2 {
+    if constexpr (MODE == MODE_FWD) {
+      return __builtin_bit_cast(uint2, *reinterpret_cast<const lds_u32x2*>(stg + off));
+    } else {
+      typedef __attribute__((ext_vector_type(2))) int i32x2_t;
+      typedef __attribute__((address_space(3))) i32x2_t lds_i32x2;
+      const i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(stg + off));
+      return __builtin_bit_cast(uint2, v);
+    }
+  };
+  // Fragment unit i (0-3 A block i, 4-7 raw B block i - 4) of the current k-step.
+  auto frag = [&](lds_char* stg, int i, uint4 (&fa)[FM], uint2 (&rb)[FN]) {
+    if (i < FM) fa[i] = read_k(stg, ao + i * 4096);
+    else rb[i - FM] = read_b8(stg, bo[i - FM]);
+  };
+  auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
+    acc[i / FN][i % FN] = Mma<TT_BF16>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
+  };
+  // Dequantisation part h (0-7): half h % 2 of raw B fragment h / 2.
+  auto deq_half = [&](int h, const uint2 (&rb)[FN], uint4 (&fb)[FN], float sc) {
+    const int u = h >> 1;
+    if (h & 1) {
+      const uint2 v = deq4(rb[u].y, sc);
+      fb[u].z = v.x;
+      fb[u].w = v.y;
+    } else {
+      const uint2 v = deq4(rb[u].x, sc);
+      fb[u].x = v.x;
+      fb[u].y = v.y;
+    }
+  };
+
+  lds_char* const lds = (lds_char*)lds_raw;
+  auto stage = [&](int g) { return lds + (g & 1) * Q_STAGE; };
+  uint4 a0[FM], b0[FN], a1[FM], b1[FN];
+  uint2 r0[FN], r1[FN];
+  float s_cur = 1.0f;  // scale of the k-tile being read
+
+  // One k-tile, as in gmm_p64_kernel: k-steps 0-2 multiply while reading
+  // (and dequantising) the next k-step, k-steps 0-1 also load the B half
+  // of k-tile kt + 1 into the other stage (one load every fourth slot); wait
+  // for k-tile kt + 1, barrier; k-step 3 multiplies while reading k-step 0 of
+  // k-tile kt + 1 and loading the A half of k-tile kt + 2 into this stage.
+  // Raw e4m3 fragments are read in slots 0-7 and dequantised in slots 8-15.
+  auto step = [&](int kt, int g, auto last_c) {
+    constexpr bool LAST = decltype(last_c)::value;
+    lds_char* const cur = stage(g);
+    lds_char* const nxt = stage(g + 1);
+    const int k1 = kt + 1, k2 = kt + 2;
+    const bool to_next1 = k1 >= nkt, to_next2 = k2 >= nkt;
+    const int kr1 = to_next1 ? k1 - nkt : k1;
+    const int kr2 = to_next2 ? k2 - nkt : k2;
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      refresh(s + 1);
+#pragma unroll
+      for (int i = 0; i < FM * FN; ++i) {
+        if (s & 1) mfma(i, a1, b1); else mfma(i, a0, b0);
+        if (i < FM + FN) {
+          if (s & 1) frag(cur, i, a0, r0); else frag(cur, i, a1, r1);
+        } else {
+          if (s & 1) deq_half(i - 8, r0, b0, s_cur); else deq_half(i - 8, r1, b1, s_cur);
+        }
+        if (s <= 1 && (i & 3) == 1) issue_one(nxt, kr1, to_next1, 4 + 4 * s + (i >> 2));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    TT_WAIT_VMCNT(0);
+    TT_LDS_BARRIER();
+    // Scale of the k-tile whose k-step 0 is read next (the next k-tile, or the
+    // next tile's first, whose scales replace this wave's row after the
+    // epilogue).
+    const float s_next = LAST ? 1.0f : sc_w[(kt + 1) >> 1];
+    refresh(0);
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+      mfma(i, a1, b1);
+      if (!LAST && i < FM + FN) frag(nxt, i, a0, r0);
+      if (!LAST && i >= FM + FN) deq_half(i - 8, r0, b0, s_next);
+      if ((i & 3) == 3) issue_one(cur, kr2, to_next2, i >> 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    s_cur = s_next;
+  };
+
+  // k-tile 0 whole and the A part of k-tile 1.
+#pragma unroll
+  for (int q = 0; q < 12; ++q) issue_one(stage(0), 0, false, q);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) issue_one(stage(1), 1, false, q);
+  TT_WAIT_VMCNT(4);
+  __builtin_amdgcn_s_barrier();
+
+  lds_char* const epi = (lds_char*)epi_raw + wave * P_EPI;
+  int g = 0;
+  for (int n = 0;;) {
+    // k-step 0 of the tile's first k-tile.
+    s_cur = sc_w[0];
+    refresh(0);
+#pragma unroll
+    for (int i = 0; i < FM + FN; ++i) frag(stage(g), i, a0, r0);
+#pragma unroll
+    for (int u = 0; u < FN; ++u) b0[u] = deq8(r0[u], s_cur);
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+    for (int kt = 0; kt < nkt - 1; ++kt, ++g) step(kt, g, std::false_type{});
+    step(nkt - 1, g, std::true_type{});
+    ++g;
+    __builtin_amdgcn_sched_barrier(0);
+    store_wave_tile_p64<TT_BF16>(acc, tc, tc.i0, tc.j0 + 128 * wave, epi);
+    if (++n == ntiles) break;
+    tc = tn;
+    ra_cur = ra_nxt;
+    rb_cur = rb_nxt;
+    sc_w[lane] = sv_next[0];
+    sc_w[lane + 64] = sv_next[1];
+    has_next = n + 1 < ntiles;
+    if (has_next) {
+      q8_tile_at<MODE>(pos + (n + 1) * G, p0, qw, out, K, N, E, tiles_j, row_start, tile_start,
+                       tn);
+      load_scales(tn, sv_next);
+    }
+    ra_nxt = rsrc_a(tn, has_next);
+    rb_nxt = rsrc_b(tn, has_next);
+  }
+  TT_WAIT_VMCNT(0);  // loads issued past the last tile land before the block exits
+}
+
 template <int MODE, bool TRANS_B>
 __global__ __launch_bounds__(256) void gmm_f32_kernel(const float* __restrict__ p0,
                                                       const float* __restrict__ p1,
@@ -1643,9 +2024,46 @@ int launch_fp8_k(const void* p0, const uint8_t* qw, const void* scale, int sdt, 
   return tt_check_launch("gmm_fp8");
 }
 
+template <int MODE, bool KMASK>
+int launch_q8_k(const void* p0, const uint8_t* qw, const void* scale, int sdt, void* out,
+                int64_t M, int64_t K, int64_t N, int E, const int64_t* counts, hipStream_t s,
+                int64_t nblk, int tj) {
+  const size_t lds = schedule_bytes(E);  // stages, staging and scale rows are static LDS
+  static size_t allowed = 64 * 1024;
+  const int rc = allow_lds(&gmm_q8_kernel<MODE, KMASK>, lds, allowed);
+  if (rc != TT_OK) return rc;
+  const int64_t cus = cu_count();
+  const int64_t grid = nblk < cus ? nblk : cus;
+  hipLaunchKernelGGL((gmm_q8_kernel<MODE, KMASK>), dim3((unsigned)grid), dim3(DM_NT), lds, s,
+                     static_cast<const char*>(p0), reinterpret_cast<const char*>(qw),
+                     static_cast<const char*>(scale), sdt, static_cast<char*>(out), M, K, N, E,
+                     counts, tj);
+  return tt_check_launch("gmm_fp8");
+}
+
 template <int MODE>
 int launch_fp8(const void* p0, const uint8_t* qw, const void* scale, int sdt, void* out, int64_t M,
                int64_t K, int64_t N, int E, const int64_t* counts, hipStream_t s) {
+  {
+    // The persistent 128x512 kernel: a reduction of at least two 64-deep
+    // k-tiles, at most Q_SMAX scale blocks along it, its LDS, and 32-bit
+    // offsets for loads that run up to two k-tiles past the reduction end.
+    const int64_t R = MODE == MODE_FWD ? K : N;
+    const int64_t J = MODE == MODE_FWD ? N : K;
+    const int64_t lda = MODE == MODE_FWD ? K : N;
+    const int tjq = (int)((J + Q_BN - 1) / Q_BN);
+    const int64_t nq = ((M + Q_BM - 1) / Q_BM + E) * (int64_t)tjq;
+    if (nq == 0) return TT_OK;
+    if (R > Q_BK && (R + 127) / 128 <= Q_SMAX &&
+        schedule_bytes(E) + 2 * Q_STAGE + 4 * P_EPI + 4 * Q_SMAX * sizeof(float) + 64 <=
+            160 * 1024 &&
+        nq < 0x7fffffff && (M + Q_BM) * lda * 2 < (int64_t)DM_OOB &&
+        (N + 2 * Q_BK + Q_BN) * K < (int64_t)DM_OOB) {
+      if (R % Q_BK)
+        return launch_q8_k<MODE, true>(p0, qw, scale, sdt, out, M, K, N, E, counts, s, nq, tjq);
+      return launch_q8_k<MODE, false>(p0, qw, scale, sdt, out, M, K, N, E, counts, s, nq, tjq);
+    }
+  }
   int ti, tj;
   const int64_t nblk = grid_blocks(MODE, true, M, K, N, E, DM_BM, DM_BN, ti, tj);
   if (nblk == 0) return TT_OK;
