@@ -143,6 +143,25 @@ int tt_swiglu_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, const voi
                   int probs_dtype, const void* grad_out, void* grad_x, void* grad_probs,
                   void* stream);
 
+/* Gated activation with an optional cap, fused with the probability
+ * weighting: act = 0 (SiLU) or 1 (GELU, erf form); limit >= 0. limit == 0:
+ * a = round(round(act(gate)) * up); limit > 0, in fp32 with one rounding:
+ * a = round(act(min(gate, limit)) * clamp(up, -limit, limit)), or with
+ * clamp_after != 0 a = round(min(act(gate), limit) * clamp(up, -limit, limit)).
+ * Then out = round(a * p) as tt_swiglu_fwd. Replaces native gated_activation
+ * (ops/providers/native/gated_activation.py:15-44) as GroupedMLP.glu calls it
+ * (models/modules/moe/experts.py:71-84) and the probability product
+ * (experts.py:181-186). */
+int tt_gated_act_fwd(const void* x, int dtype, int64_t rows, int64_t ffn, int act, float limit,
+                     int clamp_after, const void* probs, int probs_dtype, void* out,
+                     void* stream);
+
+/* Backward of tt_gated_act_fwd (autograd of the same expression; the caps
+ * pass the gradient where their input lies inside the inclusive bounds). */
+int tt_gated_act_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, int act, float limit,
+                     int clamp_after, const void* probs, int probs_dtype, const void* grad_out,
+                     void* grad_x, void* grad_probs, void* stream);
+
 /* ---- Grouped GEMM over expert segments ----------------------------------
  * Rows of x are grouped by expert: expert e owns counts[e] consecutive rows
  * (counts: device int64 [E]; sum(counts) == M). Replaces

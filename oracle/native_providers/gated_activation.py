@@ -6,7 +6,13 @@ fp32, ``up`` is clamped to ``[-limit, limit]`` and the gate is capped before
 (``act(min(gate, limit))``) or after (``min(act(gate), limit)``) activation.
 Only ``F.silu`` and ``F.gelu`` are accepted.
 
-Pinned by: closed form on hand-picked values (clamped / unclamped branches).
+``gated_activation_probs`` is the composition
+``GroupedMLP.activation_func_with_probs``
+(``src/torchturbo/models/modules/moe/experts.py:181-186``):
+``(gated_activation(x) * probs[:, None]).to(act.dtype)``.
+
+Pinned by: closed form on hand-picked values (clamped / unclamped branches),
+and gradcheck of the fp64 form away from the cap boundaries.
 """
 
 from __future__ import annotations
@@ -44,3 +50,19 @@ class TorchGatedActivation(OpImpl):
                  clamp_gate_after_activation: bool = False):
         return gated_activation(x, activation_func=activation_func, limit=limit,
                                 clamp_gate_after_activation=clamp_gate_after_activation)
+
+
+def gated_activation_probs(x, probs, *, activation_func, limit: float = 0.0,
+                           clamp_gate_after_activation: bool = False):
+    act = gated_activation(x, activation_func=activation_func, limit=limit,
+                           clamp_gate_after_activation=clamp_gate_after_activation)
+    return (act * probs.unsqueeze(-1)).to(act.dtype)
+
+
+@register_op(op_name="gated_activation_probs", impl_name="torch_gated_activation_probs",
+             kind=OpImplKind.NATIVE, priority=0, devices=())
+class TorchGatedActivationProbs(OpImpl):
+    def __call__(self, x, probs, *, activation_func, limit: float = 0.0,
+                 clamp_gate_after_activation: bool = False):
+        return gated_activation_probs(x, probs, activation_func=activation_func, limit=limit,
+                                      clamp_gate_after_activation=clamp_gate_after_activation)

@@ -171,7 +171,8 @@ def test_product_has_no_cpu_provider():
     from torchturbo_amd.dispatch import registry
     remove_provider_package("oracle.native_providers")
     d = OpDispatcher(device_runtime=CpuRuntime(), registry=registry)
-    for op in ("moe_permutation", "moe_unpermutation", "grouped_matmul", "swiglu_probs"):
+    for op in ("moe_permutation", "moe_unpermutation", "grouped_matmul", "swiglu_probs",
+               "gated_activation_probs"):
         with pytest.raises(RuntimeError, match="No implementation"):
             d._dispatch(op)
 
@@ -185,6 +186,7 @@ def test_hip_providers_registered_for_cuda_only():
     hip = [s for s in registry.list() if s.impl_name.startswith("hip_")]
     assert {s.op_name for s in hip} >= {"moe_permutation", "moe_unpermutation", "moe_sort_chunks",
                                         "grouped_matmul", "grouped_matmul_fp8", "swiglu",
-                                        "swiglu_probs", "topk_softmax_with_capacity"}
+                                        "swiglu_probs", "topk_softmax_with_capacity",
+                                        "gated_activation", "gated_activation_probs"}
     assert all(s.devices == (TurboDevice.CUDA,) and s.kind == OpImplKind.CUSTOM
                and s.priority > 100 for s in hip)

@@ -14,12 +14,14 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle.native_providers import grouped_matmul as o_gmm
 from oracle.native_providers import moe_permutation as o_perm
 from oracle.native_providers import routing as o_route
 from oracle.native_providers import swiglu as o_swiglu
 from oracle import fp8 as o_fp8
+from oracle.native_providers import gated_activation as o_gated
 from oracle import route_np
 from tests.conftest import assert_bf16_close, rel_errors
 from torchturbo_amd.dispatch import MoEPermutation
@@ -334,6 +336,50 @@ def test_swiglu_matches_oracle(hip_ops, dtype, with_probs):
     if with_probs:
         mx, mean = rel_errors(pd.grad.cpu(), pr.grad)
         assert mx <= 1e-3 and mean <= 1e-4, (mx, mean)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+@pytest.mark.parametrize("limit,after", [(0.0, False), (2.5, False), (2.5, True)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("with_probs", [False, True])
+def test_gated_activation_matches_oracle(hip_ops, act, limit, after, dtype, with_probs):
+    """GELU / capped gates (gated_activation.py:15-44) with the probability product:
+    values span the cap (|x| up to ~9) so both clamped and free branches occur."""
+    fn = F.silu if act == "silu" else F.gelu
+    rows, Fd = 257, 80
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(rows, 2 * Fd, generator=g) * 3).to(dtype)
+    p = torch.rand(rows, generator=g)
+    go = torch.randn(rows, Fd, generator=g).to(dtype)
+    kw = dict(activation_func=fn, limit=limit, clamp_gate_after_activation=after)
+    xr = x.clone().requires_grad_()
+    pr = p.clone().requires_grad_()
+    ref = (o_gated.gated_activation_probs(xr, pr, **kw) if with_probs
+           else o_gated.gated_activation(xr, **kw))
+    ref.backward(go)
+    xd = x.to(DEV).requires_grad_()
+    pd = p.to(DEV).requires_grad_()
+    got = (hip_ops.gated_activation_probs(xd, pd, **kw) if with_probs
+           else hip_ops.gated_activation(xd, **kw))
+    got.backward(go.to(DEV))
+    assert got.dtype == ref.dtype and got.shape == ref.shape
+    if dtype == torch.float32:
+        assert rel_errors(got.cpu(), ref)[0] <= 1e-5
+        assert rel_errors(xd.grad.cpu(), xr.grad)[0] <= 1e-5
+    else:
+        assert_bf16_close(got.cpu(), ref, max_rel=8e-3, mean_rel=1e-4, what="gated")
+        assert_bf16_close(xd.grad.cpu(), xr.grad, max_rel=1e-2, mean_rel=1e-3, what="dx")
+    if with_probs:
+        mx, mean = rel_errors(pd.grad.cpu(), pr.grad)
+        assert mx <= 1e-3 and mean <= 1e-4, (mx, mean)
+
+
+def test_gated_activation_rejects_like_reference(hip_ops):
+    x = torch.randn(4, 8, device=DEV)
+    with pytest.raises(ValueError, match="only supports F.silu and F.gelu"):
+        hip_ops.gated_activation(x, activation_func=torch.tanh)
+    with pytest.raises(ValueError, match="limit must be non-negative"):
+        hip_ops.gated_activation(x, activation_func=F.silu, limit=-1.0)
 
 
 # ---------------------------------------------------------------------------

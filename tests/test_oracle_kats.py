@@ -255,3 +255,39 @@ def test_gated_activation_limits():
     torch.testing.assert_close(out[0], expect)
     with pytest.raises(ValueError):
         o_gated.gated_activation(x, activation_func=torch.tanh)
+
+
+def test_gated_activation_gelu_and_probs_closed_forms():
+    # GELU gate: gelu(0) = 0 and gelu(x) -> x for large x (erf -> 1); the cap
+    # before activation turns gelu(9) into gelu(2); probs scale each row.
+    x = torch.tensor([[0.0, 9.0, 3.0, 1.5]], dtype=torch.float64)  # gate [0, 9], up [3, 1.5]
+    out = o_gated.gated_activation(x, activation_func=F.gelu)
+    assert out[0, 0].item() == 0.0
+    assert abs(out[0, 1].item() - 9.0 * 1.5) < 1e-12
+    capped = o_gated.gated_activation(x, activation_func=F.gelu, limit=2.0)
+    expect = F.gelu(torch.tensor([0.0, 2.0], dtype=torch.float64)) * torch.tensor([2.0, 1.5],
+                                                                                 dtype=torch.float64)
+    torch.testing.assert_close(capped[0].double(), expect)
+    p = torch.tensor([0.25], dtype=torch.float64)
+    withp = o_gated.gated_activation_probs(x, p, activation_func=F.gelu, limit=2.0)
+    torch.testing.assert_close(withp, capped * 0.25)
+
+
+@pytest.mark.parametrize("fn", [F.silu, F.gelu])
+@pytest.mark.parametrize("limit,after", [(0.0, False), (2.0, False), (2.0, True)])
+def test_gated_activation_probs_gradcheck(fn, limit, after):
+    # Gradients of the composition against finite differences. Without a cap
+    # the math stays fp64 (strict check); with a cap the reference computes in
+    # fp32 (``up.float()``), so the step and tolerance are sized for fp32, and
+    # the points keep away from the cap (|x| and act(x) not within 0.05 of it).
+    g = torch.Generator().manual_seed(3)
+    x = torch.rand(5, 8, generator=g, dtype=torch.float64) * 6 - 3
+    near = ((x.abs() - 2.0).abs() < 0.05) | ((fn(x) - 2.0).abs() < 0.05)
+    x = torch.where(near, x + 0.2, x).requires_grad_()
+    p = torch.rand(5, generator=g, dtype=torch.float64).requires_grad_()
+    f = lambda a, b: o_gated.gated_activation_probs(  # noqa: E731
+        a, b, activation_func=fn, limit=limit, clamp_gate_after_activation=after).double()
+    if limit == 0:
+        assert torch.autograd.gradcheck(f, (x, p))
+    else:
+        assert torch.autograd.gradcheck(f, (x, p), eps=1e-3, atol=2e-3, rtol=2e-3)

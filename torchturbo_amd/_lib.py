@@ -43,6 +43,8 @@ _PROTOS: dict[str, list] = {
     "tt_sort_chunks": [P, c_int, I64, I64, P, P, I32, P, c_int, P, P, P],
     "tt_swiglu_fwd": [P, c_int, I64, I64, P, c_int, P, P],
     "tt_swiglu_bwd": [P, c_int, I64, I64, P, c_int, P, P, P, P],
+    "tt_gated_act_fwd": [P, c_int, I64, I64, c_int, c_float, c_int, P, c_int, P, P],
+    "tt_gated_act_bwd": [P, c_int, I64, I64, c_int, c_float, c_int, P, c_int, P, P, P, P],
     "tt_gmm_fwd": [P, P, c_int, I64, I64, I64, I32, I32, P, P, P],
     "tt_gmm_dgrad": [P, P, c_int, I64, I64, I64, I32, I32, P, P, P],
     "tt_gmm_wgrad": [P, P, c_int, I64, I64, I64, I32, I32, P, P, P],

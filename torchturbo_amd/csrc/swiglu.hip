@@ -154,6 +154,140 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Gated activation with a cap (the reference's gated_activation op,
+// src/torchturbo/ops/providers/native/gated_activation.py:15-44) and the
+// probability weighting. act is SiLU or GELU (erf form); mode 0: no cap,
+//   a = round(round(act(gate)) * up)                      (16-bit rounding points)
+// mode 1 (cap before): a = round(act(min(gate, L)) * clamp(up, -L, L))   (fp32)
+// mode 2 (cap after):  a = round(min(act(gate), L) * clamp(up, -L, L))   (fp32)
+// then out = round(a * p) as in swiglu. Caps keep NaN (x > L ? L : x), and
+// their backward passes the gradient where the input lies inside the
+// (inclusive) bounds, as torch.clamp's does.
+// ---------------------------------------------------------------------------
+enum { ACT_SILU = 0, ACT_GELU = 1 };
+
+// act(g) and its derivative.
+template <class TT>
+__device__ __forceinline__ void act_eval(int act, float g, float& val, float& der) {
+  if (act == ACT_SILU) {
+    float sig, si;
+    sig_silu<TT>(g, sig, si);
+    val = si;
+    der = sig * (1.0f + g * (1.0f - sig));
+  } else {
+    const float cdf = 0.5f * (1.0f + erff(g * 0.70710678118654752f));
+    const float pdf = expf(-0.5f * g * g) * 0.39894228040143268f;
+    val = g * cdf;
+    der = cdf + g * pdf;
+  }
+}
+
+__device__ __forceinline__ float cap_hi(float x, float lim) { return x > lim ? lim : x; }
+__device__ __forceinline__ float cap_both(float x, float lim) {
+  return x < -lim ? -lim : (x > lim ? lim : x);
+}
+
+template <class TT, int PD, int V>
+__global__ __launch_bounds__(256) void gated_fwd_kernel(const typename TT::storage* __restrict__ x,
+                                                        int64_t rows, int64_t F,
+                                                        const void* __restrict__ probs, int L,
+                                                        int act, int mode, float lim,
+                                                        typename TT::storage* __restrict__ out) {
+  typedef typename TT::storage St;
+  constexpr int XD = Traits<TT>::code, PR = promote(XD, PD);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
+  if (r >= rows) return;
+  const float p = load_prob<PD>(probs, r);
+  const St* xr = x + r * 2 * F;
+  St* orow = out + r * F;
+  const int64_t nv = F / V;
+  for (int64_t v = lane & (L - 1); v < nv; v += L) {
+    St g[V], u[V], o[V];
+    load_stream<sizeof(g)>(g, xr + v * V);
+    load_stream<sizeof(u)>(u, xr + F + v * V);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const float gf = TT::to_f32(g[k]), uf = TT::to_f32(u[k]);
+      float av, der, a;
+      if (mode == 0) {
+        act_eval<TT>(act, gf, av, der);
+        a = rnd<XD>(rnd<XD>(av) * uf);
+      } else {
+        act_eval<TT>(act, mode == 1 ? cap_hi(gf, lim) : gf, av, der);
+        if (mode == 2) av = cap_hi(av, lim);
+        a = rnd<XD>(av * cap_both(uf, lim));
+      }
+      if constexpr (PD != NO_PROBS) a = rnd<PR>(a * p);
+      o[k] = TT::from_f32(a);
+    }
+    __builtin_memcpy(orow + v * V, o, sizeof(o));
+  }
+}
+
+template <class TT, int PD, int V, bool GP>
+__global__ __launch_bounds__(256) void gated_bwd_kernel(
+    const typename TT::storage* __restrict__ x, int64_t rows, int64_t F,
+    const void* __restrict__ probs, int L, int act, int mode, float lim,
+    const typename TT::storage* __restrict__ gout, typename TT::storage* __restrict__ gx,
+    void* __restrict__ gprobs) {
+  typedef typename TT::storage St;
+  constexpr int XD = Traits<TT>::code, PR = promote(XD, PD);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
+  const bool live = r < rows;  // idle lanes still join the row reduction
+  const float p = live ? load_prob<PD>(probs, r) : 0.f;
+  float dp = 0.f;
+  const int64_t nv = live ? F / V : 0;
+  const St* xr = x + r * 2 * F;
+  const St* gr = gout + r * F;
+  St* dxr = gx + r * 2 * F;
+  for (int64_t v = lane & (L - 1); v < nv; v += L) {
+    St g[V], u[V], d[V], og[V], ou[V];
+    load_stream<sizeof(g)>(g, xr + v * V);
+    load_stream<sizeof(u)>(u, xr + F + v * V);
+    load_stream<sizeof(d)>(d, gr + v * V);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const float gf = TT::to_f32(g[k]), uf = TT::to_f32(u[k]);
+      const float gd = TT::to_f32(d[k]);
+      const float da = PD != NO_PROBS ? rnd<XD>(gd * p) : gd;
+      float av, der, a, dg, du;
+      if (mode == 0) {
+        act_eval<TT>(act, gf, av, der);
+        const float sv = rnd<XD>(av);
+        a = rnd<XD>(sv * uf);
+        du = da * sv;
+        dg = rnd<XD>(da * uf) * der;
+      } else {
+        const float uc = cap_both(uf, lim);
+        const bool u_in = uf >= -lim && uf <= lim;
+        if (mode == 1) {
+          act_eval<TT>(act, cap_hi(gf, lim), av, der);
+          dg = gf <= lim ? da * uc * der : 0.f;
+        } else {
+          act_eval<TT>(act, gf, av, der);
+          const bool a_in = av <= lim;
+          av = cap_hi(av, lim);
+          dg = a_in ? da * uc * der : 0.f;
+        }
+        a = rnd<XD>(av * uc);
+        du = u_in ? da * av : 0.f;
+      }
+      if constexpr (PD != NO_PROBS && GP) dp += rnd<PR>(gd * a);
+      og[k] = TT::from_f32(dg);
+      ou[k] = TT::from_f32(du);
+    }
+    store_stream<sizeof(og)>(dxr + v * V, og);
+    store_stream<sizeof(ou)>(dxr + F + v * V, ou);
+  }
+  if constexpr (GP) {
+    for (int off = L / 2; off > 0; off >>= 1) dp += __shfl_xor(dp, off, TT_WAVE);
+    if (live && (lane & (L - 1)) == 0) store_prob<PD>(gprobs, r, dp);
+  }
+}
+
 bool float_dtype(int d) { return d == TT_F32 || d == TT_BF16 || d == TT_F16; }
 
 // Lanes per row: the power of two <= 64 that wastes the fewest lane slots
@@ -250,6 +384,103 @@ int launch_bwd(const void* x, int64_t rows, int64_t F, const void* probs, int pd
   }
 }
 
+struct GatedArgs {
+  int act, mode;
+  float lim;
+};
+
+template <class TT, int PD>
+int launch_gated_fwd_p(const void* x, int64_t rows, int64_t F, const void* probs, GatedArgs ga,
+                       void* out, hipStream_t s) {
+  typedef typename TT::storage St;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                       static_cast<uintptr_t>(F * sizeof(St));
+  const St* xp = static_cast<const St*>(x);
+  St* op = static_cast<St*>(out);
+  if (al % 16 == 0) {
+    constexpr int V = 16 / sizeof(St);
+    const int L = lanes_per_row(F / V);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((gated_fwd_kernel<TT, PD, V>), dim3((unsigned)((rows + rpb - 1) / rpb)),
+                       dim3(256), 0, s, xp, rows, F, probs, L, ga.act, ga.mode, ga.lim, op);
+  } else {
+    const int L = lanes_per_row(F);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((gated_fwd_kernel<TT, PD, 1>), dim3((unsigned)((rows + rpb - 1) / rpb)),
+                       dim3(256), 0, s, xp, rows, F, probs, L, ga.act, ga.mode, ga.lim, op);
+  }
+  return tt_check_launch("gated_activation_fwd");
+}
+
+template <class TT, int PD, bool GP>
+int launch_gated_bwd_p(const void* x, int64_t rows, int64_t F, const void* probs, GatedArgs ga,
+                       const void* gout, void* gx, void* gprobs, hipStream_t s) {
+  typedef typename TT::storage St;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gout) |
+                       reinterpret_cast<uintptr_t>(gx) | static_cast<uintptr_t>(F * sizeof(St));
+  const St* xp = static_cast<const St*>(x);
+  const St* gp = static_cast<const St*>(gout);
+  St* dxp = static_cast<St*>(gx);
+  if (al % 16 == 0) {
+    constexpr int V = 16 / sizeof(St);
+    const int L = lanes_per_row(F / V);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((gated_bwd_kernel<TT, PD, V, GP>),
+                       dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, xp, rows, F,
+                       probs, L, ga.act, ga.mode, ga.lim, gp, dxp, gprobs);
+  } else {
+    const int L = lanes_per_row(F);
+    const int64_t rpb = 4 * (64 / L);
+    hipLaunchKernelGGL((gated_bwd_kernel<TT, PD, 1, GP>),
+                       dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, xp, rows, F,
+                       probs, L, ga.act, ga.mode, ga.lim, gp, dxp, gprobs);
+  }
+  return tt_check_launch("gated_activation_bwd");
+}
+
+template <class TT>
+int launch_gated_fwd(const void* x, int64_t rows, int64_t F, const void* probs, int pdt,
+                     GatedArgs ga, void* out, hipStream_t s) {
+  if (probs == nullptr) return launch_gated_fwd_p<TT, NO_PROBS>(x, rows, F, probs, ga, out, s);
+  switch (pdt) {
+    case TT_F32: return launch_gated_fwd_p<TT, TT_F32>(x, rows, F, probs, ga, out, s);
+    case TT_BF16: return launch_gated_fwd_p<TT, TT_BF16>(x, rows, F, probs, ga, out, s);
+    default: return launch_gated_fwd_p<TT, TT_F16>(x, rows, F, probs, ga, out, s);
+  }
+}
+
+template <class TT, int PD>
+int launch_gated_bwd_g(const void* x, int64_t rows, int64_t F, const void* probs, GatedArgs ga,
+                       const void* gout, void* gx, void* gprobs, hipStream_t s) {
+  if (gprobs != nullptr)
+    return launch_gated_bwd_p<TT, PD, true>(x, rows, F, probs, ga, gout, gx, gprobs, s);
+  return launch_gated_bwd_p<TT, PD, false>(x, rows, F, probs, ga, gout, gx, gprobs, s);
+}
+
+template <class TT>
+int launch_gated_bwd(const void* x, int64_t rows, int64_t F, const void* probs, int pdt,
+                     GatedArgs ga, const void* gout, void* gx, void* gprobs, hipStream_t s) {
+  if (probs == nullptr)
+    return launch_gated_bwd_p<TT, NO_PROBS, false>(x, rows, F, probs, ga, gout, gx, gprobs, s);
+  switch (pdt) {
+    case TT_F32: return launch_gated_bwd_g<TT, TT_F32>(x, rows, F, probs, ga, gout, gx, gprobs, s);
+    case TT_BF16: return launch_gated_bwd_g<TT, TT_BF16>(x, rows, F, probs, ga, gout, gx, gprobs, s);
+    default: return launch_gated_bwd_g<TT, TT_F16>(x, rows, F, probs, ga, gout, gx, gprobs, s);
+  }
+}
+
+int gated_checks(int dtype, int64_t rows, int64_t ffn, int act, float limit, const void* probs,
+                 int probs_dtype) {
+  TT_REQUIRE(float_dtype(dtype), "gated_activation: unsupported dtype %d", dtype);
+  TT_REQUIRE(rows >= 0 && ffn >= 0, "gated_activation: negative sizes");
+  TT_REQUIRE(act == ACT_SILU || act == ACT_GELU,
+             "gated_activation only supports F.silu and F.gelu (act code %d)", act);
+  TT_REQUIRE(limit >= 0.0f, "limit must be non-negative.");
+  if (probs != nullptr)
+    TT_REQUIRE(float_dtype(probs_dtype), "gated_activation: unsupported probs dtype");
+  return TT_OK;
+}
+
 }  // namespace
 
 extern "C" int tt_swiglu_fwd(const void* x, int dtype, int64_t rows, int64_t ffn,
@@ -279,5 +510,38 @@ extern "C" int tt_swiglu_bwd(const void* x, int dtype, int64_t rows, int64_t ffn
     case TT_BF16: return launch_bwd<BF16T>(x, rows, ffn, probs, probs_dtype, grad_out, grad_x, grad_probs, s);
     case TT_F16: return launch_bwd<F16T>(x, rows, ffn, probs, probs_dtype, grad_out, grad_x, grad_probs, s);
     default: return launch_bwd<F32T>(x, rows, ffn, probs, probs_dtype, grad_out, grad_x, grad_probs, s);
+  }
+}
+
+extern "C" int tt_gated_act_fwd(const void* x, int dtype, int64_t rows, int64_t ffn, int act,
+                                float limit, int clamp_after, const void* probs,
+                                int probs_dtype, void* out, void* stream) {
+  const int rc = gated_checks(dtype, rows, ffn, act, limit, probs, probs_dtype);
+  if (rc != TT_OK) return rc;
+  if (rows == 0 || ffn == 0) return TT_OK;
+  const GatedArgs ga{act, limit == 0.0f ? 0 : (clamp_after ? 2 : 1), limit};
+  hipStream_t s = S(stream);
+  switch (dtype) {
+    case TT_BF16: return launch_gated_fwd<BF16T>(x, rows, ffn, probs, probs_dtype, ga, out, s);
+    case TT_F16: return launch_gated_fwd<F16T>(x, rows, ffn, probs, probs_dtype, ga, out, s);
+    default: return launch_gated_fwd<F32T>(x, rows, ffn, probs, probs_dtype, ga, out, s);
+  }
+}
+
+extern "C" int tt_gated_act_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, int act,
+                                float limit, int clamp_after, const void* probs,
+                                int probs_dtype, const void* grad_out, void* grad_x,
+                                void* grad_probs, void* stream) {
+  const int rc = gated_checks(dtype, rows, ffn, act, limit, probs, probs_dtype);
+  if (rc != TT_OK) return rc;
+  if (grad_probs != nullptr)
+    TT_REQUIRE(probs != nullptr, "gated_activation_bwd: grad_probs needs probs");
+  if (rows == 0) return TT_OK;
+  const GatedArgs ga{act, limit == 0.0f ? 0 : (clamp_after ? 2 : 1), limit};
+  hipStream_t s = S(stream);
+  switch (dtype) {
+    case TT_BF16: return launch_gated_bwd<BF16T>(x, rows, ffn, probs, probs_dtype, ga, grad_out, grad_x, grad_probs, s);
+    case TT_F16: return launch_gated_bwd<F16T>(x, rows, ffn, probs, probs_dtype, ga, grad_out, grad_x, grad_probs, s);
+    default: return launch_gated_bwd<F32T>(x, rows, ffn, probs, probs_dtype, ga, grad_out, grad_x, grad_probs, s);
   }
 }

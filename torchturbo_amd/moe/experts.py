@@ -8,7 +8,8 @@
   ``src/torchturbo/models/weight_converter.py:417-449``);
 * fc1 -> SwiGLU -> ``(act * probs).to(act.dtype)`` -> fc2, the probability
   product formed in the probs dtype (``experts.py:181-186``); on the GPU the
-  SwiGLU and the weighting are one fused op (``swiglu_probs``);
+  SwiGLU and the weighting are one fused op (``swiglu_probs``), and so are the
+  GELU / capped gates (``gated_activation_probs``, ``experts.py:52-84``);
 * ``moe_apply_probs_on_input`` (top-1 only) scales the inputs instead;
 * an empty input still produces (zero) weight gradients.
 
@@ -73,6 +74,12 @@ class GroupedMLP(torch.nn.Module):
         flat = probs.reshape(-1)
         if self._fused_swiglu:
             return ops.swiglu_probs(hidden_states, flat)
+        if self.config.gated_linear_unit:
+            return ops.gated_activation_probs(
+                hidden_states, flat, activation_func=self.config.activation_func,
+                limit=self.swiglu_limit,
+                clamp_gate_after_activation=self.config.moe_swiglu_clamp_gate_after_activation,
+            )
         act = self.activation_func(hidden_states)
         return (act * flat.unsqueeze(-1)).to(act.dtype)
 

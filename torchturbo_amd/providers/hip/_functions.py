@@ -261,6 +261,43 @@ class SwiGLU(torch.autograd.Function):
         return gx, gp
 
 
+class GatedActivation(torch.autograd.Function):
+    """act(gate) * up with an optional cap, and the probability product
+    (``tt_gated_act_fwd`` / ``tt_gated_act_bwd``); act 0 = SiLU, 1 = GELU."""
+
+    @staticmethod
+    def forward(ctx, x, probs, act, limit, clamp_after):
+        x = x.contiguous()
+        rows, two_f = x.shape
+        if two_f % 2:
+            raise ValueError("gated_activation expects an even last dimension")
+        F = two_f // 2
+        out = x.new_empty((rows, F))
+        pc = probs.contiguous() if probs is not None else None
+        L.call("tt_gated_act_fwd", L.ptr(x), L.dtype_code(x.dtype), rows, F, int(act),
+               float(limit), int(bool(clamp_after)), L.ptr(pc),
+               L.dtype_code(probs.dtype) if probs is not None else 0, L.ptr(out),
+               L.stream(x.device))
+        ctx.save_for_backward(x, pc)
+        ctx.cfg = (int(act), float(limit), int(bool(clamp_after)))
+        return out
+
+    @staticmethod
+    def backward(ctx, g_out):
+        x, probs = ctx.saved_tensors
+        act, limit, after = ctx.cfg
+        rows, two_f = x.shape
+        g = g_out.to(x.dtype).contiguous()
+        gx = torch.empty_like(x)
+        gp = None
+        if probs is not None and ctx.needs_input_grad[1]:
+            gp = torch.empty_like(probs)
+        L.call("tt_gated_act_bwd", L.ptr(x), L.dtype_code(x.dtype), rows, two_f // 2, act, limit,
+               after, L.ptr(probs), L.dtype_code(probs.dtype) if probs is not None else 0,
+               L.ptr(g), L.ptr(gx), L.ptr(gp), L.stream(x.device))
+        return gx, gp, None, None, None
+
+
 # ---------------------------------------------------------------------------
 # Grouped GEMM
 # ---------------------------------------------------------------------------
