@@ -2,8 +2,9 @@
 //
 // Router: one wave64 per token. Lane l owns the EPL consecutive experts
 // [l*EPL, (l+1)*EPL); top-k is k rounds of a wave arg-max (larger score
-// first, lower expert id on equal scores). Group-limited selection uses
-// segmented shuffles over the lanes of a group.
+// first, lower expert id on equal scores): a register (DPP) maximum of the
+// lanes' best remaining keys and a ballot for the lowest lane holding it.
+// Group-limited selection uses segmented shuffles over the lanes of a group.
 //
 // Routing index: packed rows are ordered by expert, then token. Three kernels:
 //   hist  : per 256-token block, per-expert counts  -> bc[E][nb]
@@ -41,6 +42,22 @@ __device__ __forceinline__ Cand cand_reduce(Cand c, int width) {
     if (better(o.sel, o.idx, c.sel, c.idx)) c = o;
   }
   return c;
+}
+
+// Wave-wide maximum in registers (DPP): butterflies within quads, half rows
+// and rows, then the row broadcasts carry the running maximum into lane 63,
+// which is read back as a uniform value. Exact (max), NaN-free inputs.
+#define TT_DPP_FMAX(v, ctrl, rmask)                                                          \
+  fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), \
+                                                       ctrl, rmask, 0xf, false)))
+__device__ __forceinline__ float wave_max_uniform(float v) {
+  v = TT_DPP_FMAX(v, 0xb1, 0xf);   // quad_perm [1, 0, 3, 2]
+  v = TT_DPP_FMAX(v, 0x4e, 0xf);   // quad_perm [2, 3, 0, 1]
+  v = TT_DPP_FMAX(v, 0x141, 0xf);  // row_half_mirror
+  v = TT_DPP_FMAX(v, 0x140, 0xf);  // row_mirror
+  v = TT_DPP_FMAX(v, 0x142, 0xa);  // row_bcast15 into rows 1 and 3
+  v = TT_DPP_FMAX(v, 0x143, 0xc);  // row_bcast31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -195,28 +212,56 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
       for (int i = 0; i < EPL; ++i)
         if (!keep) sel[i] = NEG;
     }
+    // k rounds of a wave arg-max. Each lane keeps its head: its best
+    // remaining expert (largest key, lowest id on equal keys). A round takes
+    // the wave maximum of the heads, the lowest lane holding it (ballot) and
+    // that lane's head — larger key first, lower expert id on equal keys, as
+    // a comparison of (key, id) pairs would. Only the winning lane advances.
+    float hv = NEG, hsc = 0.f, hlg = 0.f;
+    int hi = -1;
+    auto head = [&]() {
+      hv = NEG;
+      hi = -1;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (valid[i] && !taken[i] && (hi < 0 || sel[i] > hv)) {
+          hv = sel[i];
+          hi = i;
+        }
+      hsc = 0.f;
+      hlg = 0.f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (i == hi) {
+          hsc = sc[i];
+          hlg = lg[i];
+        }
+    };
+    head();
     for (int j = 0; j < K; ++j) {
-      Cand c;
-      c.sel = NEG;
-      c.idx = 0x7fffffff;
-      c.sc = 0.f;
-      c.lg = 0.f;
+      const float m = wave_max_uniform(hi >= 0 ? hv : NEG);
+      const uint64_t owners = __ballot(hi >= 0 && hv == m);
+      // K <= E valid experts, so some lane still has a head (owners is empty
+      // only for NaN keys: lane 0 then reports its head, or -1).
+      const int w = __builtin_amdgcn_readfirstlane(owners ? (int)__builtin_ctzll(owners) : 0);
+      const int wi = __builtin_amdgcn_readlane(hi, w);
+      const float wsc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hsc), w));
+      const float wlg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hlg), w));
+      if (lane == j) {
+        mine.sel = m;
+        mine.idx = w * EPL + wi;
+        mine.sc = wsc;
+        mine.lg = wlg;
+      }
+      if (lane == w) {
 #pragma unroll
-      for (int i = 0; i < EPL; ++i)
-        if (valid[i] && !taken[i] && better(sel[i], lane * EPL + i, c.sel, c.idx)) {
-          c.sel = sel[i];
-          c.idx = lane * EPL + i;
-          c.sc = sc[i];
-          c.lg = lg[i];
-        }
-      c = cand_reduce(c, TT_WAVE);
-#pragma unroll
-      for (int i = 0; i < EPL; ++i)
-        if (c.idx == lane * EPL + i) {
-          taken[i] = true;
-          slot[i] = j;
-        }
-      if (lane == j) mine = c;
+        for (int i = 0; i < EPL; ++i)
+          if (i == hi) {
+            taken[i] = true;
+            slot[i] = j;
+          }
+        head();
+      }
     }
   }
 
@@ -224,7 +269,7 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   const bool active = lane < K;
   float p;
   if (score_fn == TT_SCORE_SOFTMAX && !pre_softmax) {
-    const float mx = wave_max(active ? mine.lg : NEG);
+    const float mx = wave_max_uniform(active ? mine.lg : NEG);
     const float ex = active ? expf(mine.lg - mx) : 0.f;
     const float s = wave_sum(ex);
     p = ex / s;
