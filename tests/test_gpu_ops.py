@@ -138,8 +138,11 @@ def test_router_ties_go_to_lower_expert(hip_ops):
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("T,E,k,skew", [(1, 4, 1, False), (255, 8, 2, False), (256, 8, 2, True),
                                         (1000, 128, 8, True), (3000, 256, 8, False),
-                                        (513, 64, 16, True), (100, 1000, 3, False)])
+                                        (513, 64, 16, True), (100, 1000, 3, False),
+                                        (77, 33, 3, True), (300, 1500, 4, False)])
 def test_route_index_bit_exact(T, E, k, skew):
+    """Counting-sort row map vs the brute-force oracle; E = 33 (odd: the lane-mask
+    table's alignment) and E = 1500 (above the lane-mask limit: one ballot per expert)."""
     from torchturbo_amd.providers.hip._functions import route_index
 
     ids = distinct_ids(T, E, k, seed=T + E, skew=skew)

@@ -438,15 +438,21 @@ __global__ __launch_bounds__(64) void route_scan_kernel(int* __restrict__ bc, in
   }
 }
 
-template <int KMAX>
+// Experts up to which the rank kernel keeps a 64-bit lane mask per expert
+// and wave in LDS (4 * E * 8 bytes); beyond, it ballots once per expert.
+constexpr int kMaskExperts = 1024;
+
+template <int KMAX, bool MASKS>
 __global__ __launch_bounds__(kIdxBlock) void route_rank_kernel(
     const int64_t* __restrict__ ids, int64_t T, int K, int E, int nb, const int* __restrict__ bc,
     const int* __restrict__ totals, const void* __restrict__ probs, int pbytes,
     int32_t* __restrict__ rows_out, int32_t* __restrict__ token_of_row,
     void* __restrict__ packed_probs) {
-  extern __shared__ int smem[];
+  extern __shared__ __align__(16) int smem[];
   int* start = smem;           // [E]   first packed row of each expert
   int* wbase = smem + E;       // [4][E] per-wave base row of each expert
+  // [4][E] lane masks (MASKS), 8-byte aligned after the two int arrays.
+  uint64_t* wmask = reinterpret_cast<uint64_t*>(smem + 5 * E + (E & 1));
   __shared__ int wsum[kIdxBlock / TT_WAVE];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -505,12 +511,30 @@ __global__ __launch_bounds__(kIdxBlock) void route_rank_kernel(
   }
   __syncthreads();
 
-  // In-wave stable rank: one ballot per expert present in the wave.
+  // In-wave stable rank of lane l for expert e: popcount of the lanes below
+  // l holding e (a token selects an expert at most once).
   int row[KMAX];
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) row[j] = -1;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (TT_WAVE - lane));
-  for (int e = 0; e < E; ++e) {
+  if constexpr (MASKS) {
+    // Lane masks per expert: every lane ORs its bit into the masks of its
+    // experts (order-free, so deterministic), then reads them back. LDS
+    // operations of one wave complete in order; the waits make it explicit.
+    uint64_t* wm = wmask + (int64_t)wave * E;
+    for (int e = lane; e < E; e += TT_WAVE) wm[e] = 0ull;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      if (my[j] >= 0) atomicOr(reinterpret_cast<unsigned long long*>(&wm[my[j]]), 1ull << lane);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      if (my[j] >= 0) row[j] = wbase[wave * E + my[j]] + __popcll(wm[my[j]] & below);
+  }
+  for (int e = 0; !MASKS && e < E; ++e) {
     int slot = -1;
 #pragma unroll
     for (int j = 0; j < KMAX; ++j)
@@ -675,14 +699,23 @@ extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens,
                      expert_indices, num_tokens, topk, num_experts, nb, bc);
   hipLaunchKernelGGL(route_scan_kernel, dim3(num_experts), dim3(64), 0, s, bc, nb, num_experts,
                      totals, tokens_per_expert);
-  const size_t lds = (size_t)5 * num_experts * sizeof(int);
+  const bool masks = num_experts <= kMaskExperts;
+  const size_t lds = (size_t)5 * num_experts * sizeof(int) +
+                     (masks ? (size_t)(num_experts & 1) * 4 + (size_t)4 * num_experts * 8 : 0);
   TT_REQUIRE(lds <= 160 * 1024 - 64, "route_index: too many experts for LDS");
   const int pbytes = tt_elem_size(probs_dtype);
   const void* pd = (packed_probs != nullptr) ? probs_dense : nullptr;
-#define TT_RANK(KM)                                                                               \
-  hipLaunchKernelGGL(route_rank_kernel<KM>, dim3(nb), dim3(kIdxBlock), lds, s, expert_indices,    \
-                     num_tokens, topk, num_experts, nb, bc, totals, pd, pbytes, row_indices,      \
-                     token_of_row, packed_probs)
+#define TT_RANK(KM)                                                                              \
+  do {                                                                                           \
+    if (masks)                                                                                   \
+      hipLaunchKernelGGL((route_rank_kernel<KM, true>), dim3(nb), dim3(kIdxBlock), lds, s,       \
+                         expert_indices, num_tokens, topk, num_experts, nb, bc, totals, pd,      \
+                         pbytes, row_indices, token_of_row, packed_probs);                       \
+    else                                                                                         \
+      hipLaunchKernelGGL((route_rank_kernel<KM, false>), dim3(nb), dim3(kIdxBlock), lds, s,      \
+                         expert_indices, num_tokens, topk, num_experts, nb, bc, totals, pd,      \
+                         pbytes, row_indices, token_of_row, packed_probs);                       \
+  } while (0)
   if (topk <= 2) TT_RANK(2);
   else if (topk <= 4) TT_RANK(4);
   else if (topk <= 8) TT_RANK(8);
