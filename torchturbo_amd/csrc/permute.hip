@@ -293,22 +293,29 @@ __global__ __launch_bounds__(256) void unpermute_bwd_kernel(
   }
 }
 
-// grad_dense[t, e] = grad_packed[r_j] where e == experts[t, j], else 0.
+// grad_dense[t, e] = grad_packed[r_j] where e == experts[t, j], else 0. One
+// wave per token: the wave zeroes a private LDS row of E values, the token's
+// k lanes drop their gradients into it, and the row is written out whole.
 __global__ __launch_bounds__(256) void packed_probs_bwd_kernel(
     const void* __restrict__ gpacked, int dt, int64_t T, int K, int E,
     const int32_t* __restrict__ rows, const int64_t* __restrict__ experts,
     void* __restrict__ gdense, int64_t M) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= T * E) return;
-  const int64_t t = i / E;
-  const int e = (int)(i - t * E);
-  float v = 0.f;
-  for (int j = 0; j < K; ++j)
-    if (experts[t * K + j] == e) {
-      const int r = rows[t * K + j];
-      if (r >= 0 && r < M) v = load_as_f32(gpacked, dt, r);
-    }
-  store_from_f32(gdense, dt, i, v);
+  extern __shared__ float prow[];  // [4][E]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wave;
+  if (t >= T) return;  // whole wave; no block barrier below
+  float* row = prow + (int64_t)wave * E;
+  for (int e = lane; e < E; e += TT_WAVE) row[e] = 0.f;
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the zeros land before the values
+  __builtin_amdgcn_wave_barrier();
+  for (int j = lane; j < K; j += TT_WAVE) {
+    const int64_t e = experts[t * K + j];
+    const int r = rows[t * K + j];
+    if (e >= 0 && e < E && r >= 0 && r < M) row[e] = load_as_f32(gpacked, dt, r);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  for (int e = lane; e < E; e += TT_WAVE) store_from_f32(gdense, dt, t * E + e, row[e]);
 }
 
 // Chunk reorder: block (i, y) copies rows y, y + gridDim.y, ... of the i-th
@@ -534,8 +541,10 @@ extern "C" int tt_packed_probs_bwd(const void* grad_packed_probs, int dtype, int
              "packed_probs_bwd: bad sizes");
   const int64_t n = num_tokens * num_experts;
   if (n == 0) return TT_OK;
-  hipLaunchKernelGGL(packed_probs_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     S(stream), grad_packed_probs, dtype, num_tokens, topk, num_experts,
+  const size_t lds = (size_t)4 * num_experts * sizeof(float);
+  TT_REQUIRE(lds <= 64 * 1024, "packed_probs_bwd: too many experts (%d)", num_experts);
+  hipLaunchKernelGGL(packed_probs_bwd_kernel, dim3((unsigned)((num_tokens + 3) / 4)), dim3(256),
+                     lds, S(stream), grad_packed_probs, dtype, num_tokens, topk, num_experts,
                      row_indices, expert_indices, grad_probs_dense, num_tokens * topk);
   return tt_check_launch("packed_probs_bwd");
 }
