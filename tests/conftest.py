@@ -58,6 +58,7 @@ def process_ops(monkeypatch):
             add_provider_package("oracle.native_providers")
         else:
             remove_provider_package("oracle.native_providers")
+        ops_mod._OPS = None  # each call installs a fresh dispatcher
         return get_or_create_ops(device_runtime=runtime, default_policy=policy)
 
     yield make

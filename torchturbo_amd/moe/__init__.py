@@ -1,6 +1,7 @@
 """MoE layer stack (router, EP=1 token dispatcher, grouped experts)."""
 
 from .experts import Fp8GroupedMLP, GroupedMLP
+from .lora import GroupedLoRALinear, GroupedMLPLoRA
 from .module import ModuleSpec, build_module
 from .moe_config import MoEConfig, get_base_moe_config
 from .moe_layer import MoELayer, MoERuntimeInputs, MoESubmodules
@@ -9,7 +10,9 @@ from .token_dispatcher import MoEAlltoAllTokenDispatcher
 
 __all__ = [
     "Fp8GroupedMLP",
+    "GroupedLoRALinear",
     "GroupedMLP",
+    "GroupedMLPLoRA",
     "MoEAlltoAllTokenDispatcher",
     "MoEAuxLossAutoScaler",
     "MoEConfig",

@@ -90,6 +90,13 @@ class GroupedMLP(torch.nn.Module):
                 "`moe_apply_probs_on_input` only works with `moe_router_topk`=1."
             x = (permuted_probs.unsqueeze(-1) * x).to(x.dtype)
             permuted_probs = torch.ones_like(permuted_probs)
+        if x.nelement() == 0:
+            # No rows for these experts: dense products over the weight views keep
+            # both weights in the graph, so they still receive (zero) gradients
+            # (experts.py:255-264).
+            h = torch.matmul(x, self.weight1.view(self.config.hidden_size, -1))
+            h = self.activation_func_with_probs(h, permuted_probs)
+            return torch.matmul(h, self.weight2.view(-1, self.config.hidden_size)), None
         w1 = self.weight1.view(self.num_local_experts, self.config.hidden_size, -1)
         w2 = self.weight2.view(self.num_local_experts, -1, self.config.hidden_size)
         fc1 = ops.grouped_matmul(x, w1, tokens_per_expert, trans_b=False)
