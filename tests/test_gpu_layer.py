@@ -181,3 +181,59 @@ def test_grouped_mlp_lora_on_gpu_matches_cpu(process_ops):
         if n in ref_grads:
             mx, mean = rel_errors(p.grad.cpu(), ref_grads[n])
             assert mx <= 2e-2 and mean <= 2e-3, (n, mx, mean)
+
+
+def test_fp8_experts_loaded_from_safetensors_on_gpu(process_ops, tmp_path):
+    """HF block-FP8 expert tensors with fp32 scales, read from a safetensors file
+    into a module already on the GPU, against the reference's offline route on the
+    CPU oracle: dequantise (scripts/dequant/bailing.py:57-102), assemble
+    cat(gate, up).T / down.T (models/weight_converter.py:417-449), bf16 experts."""
+    from safetensors.torch import save_file
+
+    from oracle.fp8 import dequantize_weight, quantize_blockwise
+    from torchturbo_amd.moe import load_fp8_experts
+    from torchturbo_amd.runtime import CpuRuntime
+
+    E, H, Fd = 3, 512, 256
+    prefix = "model.layers.7.mlp.experts"
+    g = torch.Generator().manual_seed(9)
+    tensors, deq = {}, {}
+    for e in range(E):
+        for proj, shape in (("gate_proj", (Fd, H)), ("up_proj", (Fd, H)), ("down_proj", (H, Fd))):
+            q, s = quantize_blockwise(torch.randn(*shape, generator=g) * 0.05, torch.float32)
+            tensors[f"{prefix}.{e}.{proj}.weight"] = q
+            tensors[f"{prefix}.{e}.{proj}.weight_scale_inv"] = s
+            deq[e, proj] = dequantize_weight(q, s)
+    save_file(tensors, str(tmp_path / "model.safetensors"))
+    cfg = MoEConfig(hidden_size=H, moe_ffn_hidden_size=Fd, gated_linear_unit=True,
+                    activation_func=F.silu, params_dtype=torch.bfloat16)
+    counts = torch.tensor([100, 0, 157])
+    M = int(counts.sum())
+    x = (torch.randn(M, H, generator=g)).to(torch.bfloat16)
+    probs = torch.rand(M, generator=g)
+    grad = torch.randn(M, H, generator=g).to(torch.bfloat16)
+
+    process_ops(CpuRuntime(), OpPolicy.NATIVE, oracle=True)
+    ref = GroupedMLP(E, False, cfg)
+    with torch.no_grad():
+        ref.weight1.copy_(torch.cat([torch.cat([deq[e, "gate_proj"], deq[e, "up_proj"]]).T
+                                     for e in range(E)]))
+        ref.weight2.copy_(torch.cat([deq[e, "down_proj"].T for e in range(E)]))
+    xr = x.clone().requires_grad_()
+    out_r, _ = ref(xr, counts, probs)
+    out_r.backward(grad)
+
+    process_ops(CudaRuntime(), OpPolicy.CUSTOM)
+    mod = Fp8GroupedMLP(E, False, cfg).to(DEV)
+    load_fp8_experts(mod, tmp_path, prefix)
+    assert mod.s1.dtype == torch.float32 and mod.s1.device.type == "cuda"
+    xd = x.to(DEV).requires_grad_()
+    out, _ = mod(xd, counts.to(DEV), probs.to(DEV))
+    out.backward(grad.to(DEV))
+    assert_bf16_close(out.cpu(), out_r, what="fp8 ckpt out")
+    assert_bf16_close(xd.grad.cpu(), xr.grad, what="fp8 ckpt dx")
+    # master1 is [E, 2F, H] (HF out x in); weight1 is [E*H, 2F]
+    w1g = ref.weight1.grad.view(E, H, 2 * Fd).transpose(1, 2)
+    w2g = ref.weight2.grad.view(E, Fd, H).transpose(1, 2)
+    assert_bf16_close(mod.master1.grad.cpu(), w1g, what="fp8 ckpt dw1")
+    assert_bf16_close(mod.master2.grad.cpu(), w2g, what="fp8 ckpt dw2")
