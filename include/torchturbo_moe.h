@@ -58,6 +58,36 @@ int tt_router_topk_bwd(const void* logits, int logits_dtype, int64_t num_tokens,
                        int32_t pre_softmax, float scaling_factor, const int64_t* top_indices,
                        const void* grad_probs, void* grad_logits, void* stream);
 
+/* ---- Router loss statistics (aux load-balancing loss, z-loss) ------------
+ * Replaces the [T, E] work of compute_routing_scores_for_aux_loss and
+ * z_loss_func (models/modules/moe/moe_utils.py:15-70) as used by
+ * TopKRouter._apply_aux_loss / apply_z_loss (router.py:164-270); the scalar
+ * formulas on top of these sums stay with the caller. Over tokens t with
+ * padding_mask[t] == 0 (padding_mask [T] bytes, or NULL = all valid):
+ *   prob_sum [E] f32 = sum_t s_t[e], s_t the bias-free scores (softmax in
+ *     fp32; sigmoid or sqrt(softplus) divided by their sum + 1e-20);
+ *   tokens_per_expert [E] int64 = tokens whose top-k of s_t holds e (larger
+ *     first, lower expert id on equal scores);
+ *   z_sum [1] f32 = sum_t r(logsumexp(logits_t)^2), r = rounding to the
+ *     logits dtype, logsumexp formed in that dtype step by step as
+ *     torch.logsumexp does (max, x - max, exp, sum, log, + max).
+ * prob_sum and tokens_per_expert are both NULL (aux off) or both set; z_sum
+ * may be NULL (z off). Sums are reproducible (fixed grid, fixed order).
+ * Workspace: tt_router_loss_workspace(T, E) bytes. E <= 1024. */
+size_t tt_router_loss_workspace(int64_t num_tokens, int32_t num_experts);
+int tt_router_loss_fwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                       int32_t num_experts, int32_t topk, int32_t score_function,
+                       const uint8_t* padding_mask, float* prob_sum, int64_t* tokens_per_expert,
+                       float* z_sum, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward: grad_logits [T, E] (logits dtype) = d/d logits of
+ * sum_e grad_prob_sum[e] * prob_sum[e] + grad_z_sum[0] * z_sum; either grad
+ * pointer may be NULL (that term is absent). Padding tokens get zeros. */
+int tt_router_loss_bwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                       int32_t num_experts, int32_t score_function, const uint8_t* padding_mask,
+                       const float* grad_prob_sum, const float* grad_z_sum, void* grad_logits,
+                       void* stream);
+
 /* ---- Routing index (counting sort by expert) ----------------------------
  * Replaces the index build of TorchMoEMaskPermutation
  * (ops/providers/native/moe_permutation.py:36-56: masked_select of token ids,

@@ -116,3 +116,55 @@ def topk_softmax_with_capacity(
 class TorchTopKSoftmax(OpImpl):
     def __call__(self, logits, topk, **kwargs):
         return topk_softmax_with_capacity(logits, topk, **kwargs)
+
+
+def router_loss_stats(logits, topk, score_function="softmax", padding_mask=None, *,
+                      aux=True, z=True):
+    """The [T, E] sums behind the router's aux loss and z-loss.
+
+    ``prob_sum`` / ``tokens_per_expert`` are ``scores.sum(0)`` and
+    ``routing_map.sum(0)`` of ``compute_routing_scores_for_aux_loss``
+    (``models/modules/moe/moe_utils.py:15-43``, bias-free scores, padding rows
+    zeroed); ``z_sum`` is the fp32 sum of the valid rows of
+    ``square(logsumexp(logits))`` (``moe_utils.py:61-68``), each value in the
+    logits dtype. Switched-off parts are zeros.
+
+    Pinned by: the aux/z KATs of ``tests/models/test_moe_router.py`` restated in
+    ``tests/test_oracle_kats.py`` and closed forms on tiny inputs there.
+    """
+    logits = logits.reshape(-1, logits.size(-1))
+    num_experts = logits.shape[1]
+    prob_sum = torch.zeros(num_experts, dtype=torch.float32, device=logits.device)
+    counts = torch.zeros(num_experts, dtype=torch.int64, device=logits.device)
+    z_sum = torch.zeros((), dtype=torch.float32, device=logits.device)
+    valid = None if padding_mask is None else (~padding_mask.reshape(-1).bool()).unsqueeze(-1)
+    if aux:
+        if score_function == "softmax":
+            scores = torch.softmax(logits, dim=-1, dtype=torch.float32)
+        elif score_function in ("sigmoid", "sqrtsoftplus"):
+            scores = (torch.sigmoid(logits.float()) if score_function == "sigmoid"
+                      else F.softplus(logits.float()).sqrt())
+            scores = scores / (scores.sum(dim=-1, keepdim=True) + 1e-20)
+        else:
+            raise ValueError(f"Invalid score_function: {score_function}")
+        top = torch.topk(scores, k=topk, dim=-1).indices
+        routing_map = torch.zeros_like(logits, dtype=torch.int32).scatter_(1, top, 1).bool()
+        if valid is not None:
+            scores = scores * valid
+            routing_map = (routing_map * valid).bool()
+        prob_sum = scores.sum(dim=0)
+        counts = routing_map.sum(dim=0)
+    if z:
+        values = torch.square(torch.logsumexp(logits, dim=-1))
+        if valid is not None:
+            values = values * valid.squeeze(-1)
+        z_sum = values.float().sum()
+    return prob_sum, counts, z_sum
+
+
+@register_op(op_name="router_loss_stats", impl_name="torch_router_loss_stats",
+             kind=OpImplKind.NATIVE, priority=0, devices=())
+class TorchRouterLossStats(OpImpl):
+    def __call__(self, logits, topk, score_function="softmax", padding_mask=None, *, aux=True,
+                 z=True):
+        return router_loss_stats(logits, topk, score_function, padding_mask, aux=aux, z=z)

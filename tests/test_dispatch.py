@@ -172,7 +172,7 @@ def test_product_has_no_cpu_provider():
     remove_provider_package("oracle.native_providers")
     d = OpDispatcher(device_runtime=CpuRuntime(), registry=registry)
     for op in ("moe_permutation", "moe_unpermutation", "grouped_matmul", "swiglu_probs",
-               "gated_activation_probs"):
+               "gated_activation_probs", "router_loss_stats"):
         with pytest.raises(RuntimeError, match="No implementation"):
             d._dispatch(op)
 
@@ -187,6 +187,7 @@ def test_hip_providers_registered_for_cuda_only():
     assert {s.op_name for s in hip} >= {"moe_permutation", "moe_unpermutation", "moe_sort_chunks",
                                         "grouped_matmul", "grouped_matmul_fp8", "swiglu",
                                         "swiglu_probs", "topk_softmax_with_capacity",
-                                        "gated_activation", "gated_activation_probs"}
+                                        "gated_activation", "gated_activation_probs",
+                                        "router_loss_stats"}
     assert all(s.devices == (TurboDevice.CUDA,) and s.kind == OpImplKind.CUSTOM
                and s.priority > 100 for s in hip)

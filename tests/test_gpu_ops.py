@@ -24,7 +24,7 @@ from oracle import fp8 as o_fp8
 from oracle.native_providers import gated_activation as o_gated
 from oracle import route_np
 from tests.conftest import assert_bf16_close, rel_errors
-from torchturbo_amd.dispatch import MoEPermutation
+from torchturbo_amd.dispatch import MoEPermutation, OpPolicy
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -131,6 +131,113 @@ def test_router_ties_go_to_lower_expert(hip_ops):
     logits = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0]], device=DEV)
     _, _, ids = hip_ops.topk_softmax_with_capacity(logits, 2)
     assert ids.cpu().tolist() == [[1, 2]]
+
+
+# T, E, k, score function, logits dtype, padded rows
+LOSS_CASES = [
+    (1000, 128, 8, "softmax", torch.float32, False),
+    (777, 33, 3, "sigmoid", torch.float32, True),
+    (513, 256, 8, "sigmoid", torch.float32, False),
+    (300, 160, 6, "sqrtsoftplus", torch.float32, True),
+    (20000, 64, 4, "softmax", torch.float32, True),  # several tokens per wave
+    (1024, 128, 8, "softmax", torch.bfloat16, False),
+    (5, 1024, 1, "sigmoid", torch.float32, False),
+    (0, 16, 2, "softmax", torch.float32, False),
+]
+
+
+@pytest.mark.parametrize("case", LOSS_CASES, ids=lambda c: f"{c[0]}x{c[1]}k{c[2]}-{c[3]}-{c[4]}")
+def test_router_loss_stats_matches_oracle(hip_ops, case):
+    """Aux/z-loss sums (moe_utils.py:15-70) vs the oracle: counts bit-exact
+    for fp32 logits, score sums and z within fp32 rounding, and the one-pass
+    backward vs autograd of the oracle composition."""
+    T, E, k, score, dtype, padded = case
+    g = torch.Generator().manual_seed(T + 7 * E)
+    logits = (torch.randn(T, E, generator=g) * 2).to(dtype)
+    pad = (torch.rand(T, generator=g) < 0.2) if padded else None
+    ref = logits.clone().requires_grad_()
+    ps_r, cn_r, zs_r = o_route.router_loss_stats(ref, k, score, pad)
+    dev = logits.to(DEV).requires_grad_()
+    ps, cn, zs = hip_ops.router_loss_stats(dev, k, score, None if pad is None else pad.to(DEV))
+    assert ps.dtype == torch.float32 and cn.dtype == torch.int64 and zs.dim() == 0
+    n_valid = T - (int(pad.sum()) if pad is not None else 0)
+    assert int(cn.sum()) == k * n_valid
+    if dtype == torch.float32:
+        assert torch.equal(cn.cpu(), cn_r)
+    else:
+        # bf16 logits tie; only rows with a tie at the k-th score may differ
+        s = torch.softmax(logits.float(), -1).sort(dim=1, descending=True).values
+        ties = int((s[:, k - 1] == s[:, k]).sum())
+        assert int((cn.cpu() - cn_r).abs().sum()) <= 2 * ties
+    torch.testing.assert_close(ps.cpu(), ps_r, rtol=1e-5, atol=1e-5)
+    ztol = 1e-5 if dtype == torch.float32 else 2e-3
+    torch.testing.assert_close(zs.cpu(), zs_r, rtol=ztol, atol=1e-5)
+    gp = torch.randn(E, generator=g)
+    gz = torch.randn((), generator=g)
+    ((ps_r * gp).sum() + zs_r * gz).backward()
+    ((ps * gp.to(DEV)).sum() + zs * gz.to(DEV)).backward()
+    if T == 0:
+        assert dev.grad.shape == (0, E)
+        return
+    if pad is not None:
+        assert not dev.grad.cpu()[pad].any()
+    if dtype == torch.float32:
+        mx, mean = rel_errors(dev.grad.cpu(), ref.grad)
+        assert mx <= 2e-5 and mean <= 2e-6, (mx, mean)
+    else:
+        assert_bf16_close(dev.grad.cpu(), ref.grad, what="dlogits")
+
+
+def test_router_loss_stats_is_reproducible(hip_ops):
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn(50000, 128, generator=g).to(DEV)
+    a = hip_ops.router_loss_stats(logits, 8, "softmax")
+    b = hip_ops.router_loss_stats(logits, 8, "softmax")
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_router_aux_and_z_losses_on_gpu_match_cpu(process_ops, monkeypatch):
+    """TopKRouter with both losses (router.py:164-356) through the HIP ops vs the
+    same router on the CPU oracle: probs, loss metrics, weight and input grads."""
+    from torchturbo_amd.moe import MoEConfig, TopKRouter
+    from torchturbo_amd.moe.router import MoEAuxLossAutoScaler
+    from torchturbo_amd.runtime import CpuRuntime, CudaRuntime
+
+    monkeypatch.setattr(MoEAuxLossAutoScaler, "loss_scale", 1.0)
+    # seed 4: every token's 8th and 9th logits differ by >= 2.8e-4, far above
+    # the rounding difference of the CPU and GPU fp32 gating GEMMs
+    torch.manual_seed(4)
+    cfg = MoEConfig(hidden_size=64, num_moe_experts=128, moe_router_topk=8,
+                    moe_router_dtype="fp32", moe_aux_loss_coeff=0.01, moe_z_loss_coeff=0.001,
+                    params_dtype=torch.float32)
+    router = TopKRouter(cfg)
+    torch.nn.init.normal_(router.weight, std=0.2)
+    x = torch.randn(4, 128, 64)
+    w = torch.randn(512, 128)
+
+    process_ops(CpuRuntime(), OpPolicy.NATIVE, oracle=True)
+    xr = x.clone().requires_grad_()
+    pr, mr, _, _ = router(xr)
+    (pr * w).sum().backward()
+    m_ref = router.pop_metrics()
+    gw_ref = router.weight.grad.clone()
+
+    process_ops(CudaRuntime(), OpPolicy.CUSTOM)
+    router = router.to(DEV)
+    router.weight.grad = None
+    xd = x.to(DEV).requires_grad_()
+    pd, md, _, _ = router(xd)
+    (pd * w.to(DEV)).sum().backward()
+    m = router.pop_metrics()
+    assert torch.equal(md.cpu(), mr)
+    torch.testing.assert_close(pd.cpu(), pr, rtol=1e-5, atol=1e-6)
+    for key in ("aux_loss", "aux_loss_scaled", "z_loss", "z_loss_scaled"):
+        torch.testing.assert_close(m[key].cpu(), m_ref[key], rtol=1e-5, atol=0)
+    mx, _ = rel_errors(router.weight.grad.cpu(), gw_ref)
+    assert mx <= 1e-4, mx
+    mx, _ = rel_errors(xd.grad.cpu(), xr.grad)
+    assert mx <= 1e-4, mx
 
 
 # ---------------------------------------------------------------------------

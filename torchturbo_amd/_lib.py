@@ -35,6 +35,9 @@ _PROTOS: dict[str, list] = {
     "tt_router_topk_fwd": [P, c_int, I64, I32, I32, I32, I32, P, I32, I32, c_float, P, P, P, P, P],
     "tt_router_topk_bwd": [P, c_int, I64, I32, I32, I32, I32, c_float, P, P, P, P],
     "tt_route_index_workspace": [I64, I32],
+    "tt_router_loss_workspace": [I64, I32],
+    "tt_router_loss_fwd": [P, c_int, I64, I32, I32, I32, P, P, P, P, P, c_size_t, P],
+    "tt_router_loss_bwd": [P, c_int, I64, I32, I32, P, P, P, P, P],
     "tt_route_index": [P, I64, I32, I32, P, c_int, P, P, P, P, P, c_size_t, P],
     "tt_permute_scatter": [P, c_int, I64, I64, I32, P, P, P],
     "tt_unpermute_gather": [P, c_int, I64, I64, I32, P, P, P, c_int, I32, P, P],
@@ -51,7 +54,8 @@ _PROTOS: dict[str, list] = {
     "tt_gmm_fp8_fwd": [P, P, P, c_int, I64, I64, I64, I32, P, P, P],
     "tt_gmm_fp8_dgrad": [P, P, P, c_int, I64, I64, I64, I32, P, P, P],
 }
-_RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_route_index_workspace": c_size_t}
+_RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_route_index_workspace": c_size_t,
+             "tt_router_loss_workspace": c_size_t}
 ABI_VERSION = 1
 
 _LIB: ctypes.CDLL | None = None
@@ -146,3 +150,7 @@ def stream(device: torch.device | None = None):
 
 def route_index_workspace(num_tokens: int, num_experts: int) -> int:
     return int(load().tt_route_index_workspace(num_tokens, num_experts))
+
+
+def router_loss_workspace(num_tokens: int, num_experts: int) -> int:
+    return int(load().tt_router_loss_workspace(num_tokens, num_experts))

@@ -392,6 +392,314 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Router loss statistics: what the load-balancing (aux) loss and the z-loss
+// need from the [T, E] logits, in one pass (models/modules/moe/moe_utils.py:
+// 15-70, router.py:164-270).
+//   prob_sum[e] = sum over valid tokens of the bias-free score s_t[e]
+//                 (softmax in fp32; sigmoid or sqrt(softplus) divided by
+//                 their sum + 1e-20);
+//   counts[e]   = valid tokens whose top-k of s_t (larger first, lower id on
+//                 equal scores) holds e;
+//   z_sum       = sum over valid tokens of r(lse_t^2), r the rounding to
+//                 the logits dtype, lse_t formed as torch.logsumexp forms it
+//                 in that dtype (the reference's logsumexp and square run in
+//                 the logits dtype).
+// Each wave walks tokens wave, wave + W, ... of a grid whose size depends on
+// T only; per-block partial rows are summed in block order by a one-block
+// kernel, so the results are reproducible.
+// ---------------------------------------------------------------------------
+constexpr int kLossWaves = 4;
+constexpr int kLossMaxBlocks = 512;
+constexpr int kLossTokensPerWave = 8;
+
+int loss_blocks(int64_t T) {
+  const int64_t per = (int64_t)kLossWaves * kLossTokensPerWave;
+  const int64_t nb = (T + per - 1) / per;
+  return (int)(nb < 1 ? 1 : (nb > kLossMaxBlocks ? kLossMaxBlocks : nb));
+}
+
+// log-sum-exp of a token's logits as PyTorch forms it: fp32 logits
+// max + log(sum exp(x - max)); bf16 / f16 logits run every step in that
+// dtype (max, x - max, exp, sum, log, + max each rounded), which is what
+// torch.logsumexp does for them. se is the fp32 sum of exp(x - mx).
+template <int EPL>
+__device__ __forceinline__ float lse_like_torch(const float (&lg)[EPL], const bool (&valid)[EPL],
+                                                float mx, float se, int ldt) {
+  if (ldt == TT_F32) return mx + logf(se);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    if (valid[i]) s += round_to(expf(round_to(lg[i] - mx, ldt)), ldt);
+  s = round_to(wave_sum(s), ldt);
+  return round_to(round_to(logf(s), ldt) + mx, ldt);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void router_loss_fwd_kernel(
+    const void* __restrict__ logits, int ldt, int64_t T, int E, int K, int score_fn,
+    const uint8_t* __restrict__ pad, int want_aux, int want_z, float* __restrict__ part_p,
+    int* __restrict__ part_c, float* __restrict__ part_z) {
+  extern __shared__ __align__(16) float lsm[];  // [4][E] prob sums, [4][E] counts, [4] z
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const float NEG = -INFINITY;
+  float ps[EPL];
+  int cn[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    ps[i] = 0.f;
+    cn[i] = 0;
+  }
+  float zs = 0.f;
+  const int64_t stride = (int64_t)gridDim.x * kLossWaves;
+  for (int64_t t = (int64_t)blockIdx.x * kLossWaves + wave; t < T; t += stride) {
+    if (pad != nullptr && pad[t] != 0) continue;  // wave-uniform
+    float lg[EPL], ex[EPL];
+    bool valid[EPL];
+    float mx = NEG;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane * EPL + i;
+      valid[i] = e < E;
+      lg[i] = valid[i] ? load_as_f32(logits, ldt, t * E + e) : NEG;
+      mx = fmaxf(mx, lg[i]);
+    }
+    mx = wave_max_uniform(mx);
+    float se = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      ex[i] = valid[i] ? expf(lg[i] - mx) : 0.f;
+      se += ex[i];
+    }
+    se = wave_sum(se);
+    if (want_z) {
+      const float lse = lse_like_torch(lg, valid, mx, se, ldt);
+      zs += round_to(lse * lse, ldt);
+    }
+    if (!want_aux) continue;
+    float sc[EPL];
+    if (score_fn == TT_SCORE_SOFTMAX) {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) sc[i] = ex[i] / se;
+    } else {
+      float den = 0.f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        sc[i] = !valid[i] ? 0.f
+                : score_fn == TT_SCORE_SIGMOID ? sigmoid_f(lg[i])
+                                               : sqrtf(softplus_f(lg[i]));
+        den += sc[i];
+      }
+      den = wave_sum(den) + 1e-20f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) sc[i] = sc[i] / den;
+    }
+    // Top-k of the scores: k rounds of the wave arg-max of the lanes' heads
+    // (best remaining expert of each lane), as in router_fwd_kernel.
+    bool taken[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) taken[i] = false;
+    float hv = NEG;
+    int hi = -1;
+    auto head = [&]() {
+      hv = NEG;
+      hi = -1;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (valid[i] && !taken[i] && (hi < 0 || sc[i] > hv)) {
+          hv = sc[i];
+          hi = i;
+        }
+    };
+    head();
+    for (int j = 0; j < K; ++j) {
+      const float m = wave_max_uniform(hi >= 0 ? hv : NEG);
+      const uint64_t owners = __ballot(hi >= 0 && hv == m);
+      const int w = __builtin_amdgcn_readfirstlane(owners ? (int)__builtin_ctzll(owners) : 0);
+      if (lane == w) {
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          if (i == hi) taken[i] = true;
+        head();
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      ps[i] += sc[i];
+      cn[i] += taken[i] ? 1 : 0;
+    }
+  }
+  // Combine the block's four waves in wave order.
+  float* sp = lsm;
+  int* scn = reinterpret_cast<int*>(lsm + kLossWaves * E);
+  float* sz = lsm + 2 * kLossWaves * E;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane * EPL + i;
+    if (e < E) {
+      sp[wave * E + e] = ps[i];
+      scn[wave * E + e] = cn[i];
+    }
+  }
+  if (lane == 0) sz[wave] = zs;
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float p = 0.f;
+    int c = 0;
+    for (int w = 0; w < kLossWaves; ++w) {
+      p += sp[w * E + e];
+      c += scn[w * E + e];
+    }
+    part_p[(int64_t)blockIdx.x * E + e] = p;
+    part_c[(int64_t)blockIdx.x * E + e] = c;
+  }
+  if (threadIdx.x == 0) {
+    float z = 0.f;
+    for (int w = 0; w < kLossWaves; ++w) z += sz[w];
+    part_z[blockIdx.x] = z;
+  }
+}
+
+// One wave per expert (block e < E) and one for z (block E): lane l sums the
+// partial rows l, l + 64, ... in order, then a butterfly adds the lanes, so
+// the result does not depend on scheduling.
+__global__ __launch_bounds__(64) void router_loss_reduce_kernel(
+    const float* __restrict__ part_p, const int* __restrict__ part_c,
+    const float* __restrict__ part_z, int nb, int E, float* __restrict__ prob_sum,
+    int64_t* __restrict__ counts, float* __restrict__ z_sum) {
+  const int lane = threadIdx.x;
+  const int e = blockIdx.x;
+  if (e < E) {
+    if (prob_sum == nullptr) return;
+    float p = 0.f;
+    int c = 0;
+    for (int b = lane; b < nb; b += TT_WAVE) {
+      p += part_p[(int64_t)b * E + e];
+      c += part_c[(int64_t)b * E + e];
+    }
+    p = wave_sum(p);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, TT_WAVE);
+    if (lane == 0) {
+      prob_sum[e] = p;
+      counts[e] = c;
+    }
+  } else if (z_sum != nullptr) {
+    float z = 0.f;
+    for (int b = lane; b < nb; b += TT_WAVE) z += part_z[b];
+    z = wave_sum(z);
+    if (lane == 0) *z_sum = z;
+  }
+}
+
+// d logits of  sum_e g_p[e] * prob_sum[e] + g_z * z_sum  (one wave per token;
+// padding tokens get zeros). Softmax scores: s * (g - <s, g>); normalised
+// sigmoid / sqrt(softplus) r / (sum r + 1e-20): dr = g / D - <g, r> / D^2,
+// then r' = r (1 - r) or softplus' / (2 r); z: g_z * 2 r(lse) * softmax.
+// For bf16 / f16 logits the two terms follow the reference's autograd in
+// that dtype: the aux term is the fp32 score gradient rounded once (the
+// backward of the cast to fp32); the z term rounds where PyTorch's bf16 ops
+// do: g = r(g_z), square: r(g * 2 lse), logsumexp: r(g' * r(exp(r(x - lse))))
+// (moe_utils.py:61-70); the sum of the two is rounded as autograd's add.
+template <int EPL>
+__global__ __launch_bounds__(256) void router_loss_bwd_kernel(
+    const void* __restrict__ logits, int ldt, int64_t T, int E, int score_fn,
+    const uint8_t* __restrict__ pad, const float* __restrict__ g_p, const float* __restrict__ g_z,
+    void* __restrict__ grad_logits) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float NEG = -INFINITY;
+  float out[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) out[i] = 0.f;
+  if (pad == nullptr || pad[t] == 0) {
+    float lg[EPL], ex[EPL];
+    bool valid[EPL];
+    float mx = NEG;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane * EPL + i;
+      valid[i] = e < E;
+      lg[i] = valid[i] ? load_as_f32(logits, ldt, t * E + e) : NEG;
+      mx = fmaxf(mx, lg[i]);
+    }
+    mx = wave_max_uniform(mx);
+    float se = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      ex[i] = valid[i] ? expf(lg[i] - mx) : 0.f;
+      se += ex[i];
+    }
+    se = wave_sum(se);
+    const bool low = ldt != TT_F32;
+    float zt[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) zt[i] = 0.f;
+    if (g_z != nullptr) {
+      const float lse = lse_like_torch(lg, valid, mx, se, ldt);
+      if (low) {
+        const float gl = round_to(round_to(*g_z, ldt) * (2.f * lse), ldt);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          zt[i] = valid[i] ? round_to(gl * round_to(expf(round_to(lg[i] - lse, ldt)), ldt), ldt)
+                           : 0.f;
+      } else {
+        const float f = *g_z * 2.f * lse;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) zt[i] = f * (ex[i] / se);
+      }
+    }
+    if (g_p != nullptr) {
+      float g[EPL];
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) g[i] = valid[i] ? g_p[lane * EPL + i] : 0.f;
+      if (score_fn == TT_SCORE_SOFTMAX) {
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) dot += (ex[i] / se) * g[i];
+        dot = wave_sum(dot);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) out[i] += (ex[i] / se) * (g[i] - dot);
+      } else {
+        float r[EPL];
+        float den = 0.f, dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+          r[i] = !valid[i] ? 0.f
+                 : score_fn == TT_SCORE_SIGMOID ? sigmoid_f(lg[i])
+                                                : sqrtf(softplus_f(lg[i]));
+          den += r[i];
+          dot += g[i] * r[i];
+        }
+        den = wave_sum(den) + 1e-20f;
+        dot = wave_sum(dot);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+          if (!valid[i]) continue;
+          const float dr = g[i] / den - dot / (den * den);
+          float d;
+          if (score_fn == TT_SCORE_SIGMOID) {
+            d = r[i] * (1.0f - r[i]);
+          } else {
+            const float dsp = lg[i] > 20.0f ? 1.0f : sigmoid_f(lg[i]);
+            d = r[i] > 0.f ? dsp / (2.0f * r[i]) : 0.f;
+          }
+          out[i] += dr * d;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) out[i] = (low ? round_to(out[i], ldt) : out[i]) + zt[i];
+  }
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane * EPL + i;
+    if (e < E) store_from_f32(grad_logits, ldt, t * E + e, out[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Routing index.
 // ---------------------------------------------------------------------------
 constexpr int kIdxBlock = 256;  // tokens per block
@@ -723,4 +1031,83 @@ extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens,
   else TT_RANK(64);
 #undef TT_RANK
   return tt_check_launch("route_rank");
+}
+
+extern "C" size_t tt_router_loss_workspace(int64_t num_tokens, int32_t num_experts) {
+  const int64_t nb = loss_blocks(num_tokens);
+  return (size_t)(nb * num_experts * 2 + nb) * 4 + 256;
+}
+
+extern "C" int tt_router_loss_fwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                                  int32_t num_experts, int32_t topk, int32_t score_function,
+                                  const uint8_t* padding_mask, float* prob_sum,
+                                  int64_t* tokens_per_expert, float* z_sum, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  TT_REQUIRE(float_dtype(logits_dtype), "router_loss: unsupported logits dtype %d", logits_dtype);
+  TT_REQUIRE(num_tokens >= 0, "router_loss: negative token count");
+  TT_REQUIRE(num_experts >= 1 && num_experts <= 1024,
+             "router_loss: num_experts must be in [1, 1024]");
+  TT_REQUIRE(score_function >= 0 && score_function <= 2, "router_loss: bad score function");
+  TT_REQUIRE((prob_sum == nullptr) == (tokens_per_expert == nullptr),
+             "router_loss: prob_sum and tokens_per_expert go together");
+  if (prob_sum != nullptr)
+    TT_REQUIRE(topk >= 1 && topk <= num_experts, "router_loss: topk must be in [1, E]");
+  TT_REQUIRE(workspace_bytes >= tt_router_loss_workspace(num_tokens, num_experts),
+             "router_loss: workspace too small");
+  if (prob_sum == nullptr && z_sum == nullptr) return TT_OK;
+  hipStream_t s = S(stream);
+  const int nb = loss_blocks(num_tokens);
+  float* part_p = static_cast<float*>(workspace);
+  int* part_c = reinterpret_cast<int*>(part_p + (int64_t)nb * num_experts);
+  float* part_z = reinterpret_cast<float*>(part_c + (int64_t)nb * num_experts);
+  int used = 0;
+  if (num_tokens > 0) {
+    const size_t lds = (size_t)(2 * kLossWaves * num_experts + kLossWaves) * 4;
+    const int aux = prob_sum != nullptr, zz = z_sum != nullptr;
+    switch (epl_for(num_experts)) {
+#define TT_CASE(N)                                                                             \
+  case N:                                                                                      \
+    hipLaunchKernelGGL(router_loss_fwd_kernel<N>, dim3(nb), dim3(256), lds, s, logits,         \
+                       logits_dtype, num_tokens, num_experts, topk, score_function,            \
+                       padding_mask, aux, zz, part_p, part_c, part_z);                         \
+    break;
+      TT_CASE(1) TT_CASE(2) TT_CASE(4) TT_CASE(8) TT_CASE(16)
+#undef TT_CASE
+      default:
+        tt_set_error("router_loss: unsupported expert count");
+        return TT_ERR_UNSUPPORTED;
+    }
+    used = nb;
+  }
+  hipLaunchKernelGGL(router_loss_reduce_kernel, dim3(num_experts + 1), dim3(64), 0, s, part_p,
+                     part_c, part_z, used, num_experts, prob_sum, tokens_per_expert, z_sum);
+  return tt_check_launch("router_loss_fwd");
+}
+
+extern "C" int tt_router_loss_bwd(const void* logits, int logits_dtype, int64_t num_tokens,
+                                  int32_t num_experts, int32_t score_function,
+                                  const uint8_t* padding_mask, const float* grad_prob_sum,
+                                  const float* grad_z_sum, void* grad_logits, void* stream) {
+  TT_REQUIRE(float_dtype(logits_dtype), "router_loss_bwd: unsupported logits dtype %d",
+             logits_dtype);
+  TT_REQUIRE(num_tokens >= 0, "router_loss_bwd: negative token count");
+  TT_REQUIRE(num_experts >= 1 && num_experts <= 1024,
+             "router_loss_bwd: num_experts must be in [1, 1024]");
+  TT_REQUIRE(score_function >= 0 && score_function <= 2, "router_loss_bwd: bad score function");
+  if (num_tokens == 0) return TT_OK;
+  const dim3 grid((unsigned)((num_tokens + kRouterWaves - 1) / kRouterWaves));
+  switch (epl_for(num_experts)) {
+#define TT_CASE(N)                                                                               \
+  case N:                                                                                        \
+    hipLaunchKernelGGL(router_loss_bwd_kernel<N>, grid, dim3(256), 0, S(stream), logits,         \
+                       logits_dtype, num_tokens, num_experts, score_function, padding_mask,      \
+                       grad_prob_sum, grad_z_sum, grad_logits);                                  \
+    break;
+    TT_CASE(1) TT_CASE(2) TT_CASE(4) TT_CASE(8) TT_CASE(16)
+#undef TT_CASE
+    default:
+      tt_set_error("router_loss_bwd: unsupported expert count");
+      return TT_ERR_UNSUPPORTED;
+  }
+  return tt_check_launch("router_loss_bwd");
 }

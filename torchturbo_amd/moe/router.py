@@ -5,8 +5,13 @@ the gating linear runs in the router dtype with autocast off and recomputes
 its casts in backward (``:25-58``); ``routing`` applies the z-loss, calls the
 top-k selection, attaches the aux loss and accumulates expert-bias counts
 (``:277-356``). Top-k selection goes through the ``topk_softmax_with_capacity``
-op so the GPU runs the fused HIP router kernel; the aux/z-loss statistics
-stay in PyTorch, as in the reference.
+op, and the [T, E] sums behind the aux loss and the z-loss (per-expert score
+sums and top-k counts of the bias-free scores, the sum of squared
+log-sum-exps) through the ``router_loss_stats`` op, so the GPU runs one HIP
+kernel for each per direction. The scalar formulas on top of those sums, the
+sequence-parallel all-reduce and the metrics are the reference's
+(``router.py:164-270``). ``compute_routing_scores_for_aux_loss`` and
+``z_loss_func`` (``moe_utils.py:15-70``) remain importable.
 """
 
 from __future__ import annotations
@@ -157,35 +162,45 @@ class TopKRouter(Router):
         if getattr(self, "expert_bias", None) is not None and self.expert_bias.dtype != torch.float32:
             self.expert_bias.data = self.expert_bias.data.to(torch.float32)
 
-    def _apply_aux_loss(self, probs, scores, routing_map):
+    def _apply_aux_loss(self, probs, prob_sum, tokens_per_expert):
+        """``router.py:180-223`` with ``prob_sum = scores.sum(0)`` and
+        ``tokens_per_expert = routing_map.sum(0)`` already reduced
+        (``router_loss_stats``)."""
         coeff = self.config.moe_aux_loss_coeff
         if coeff == 0.0:
             return probs
-        tokens_per_expert = routing_map.sum(dim=0)
         sp_size = _group_size(self.sp_group)
         if sp_size > 1:
             dist.all_reduce(tokens_per_expert, op=dist.ReduceOp.SUM, group=self.sp_group)
         total = (tokens_per_expert.sum() / self.topk).clamp_min(1)
-        raw = (torch.sum(scores.sum(dim=0) * tokens_per_expert) * self.num_experts * sp_size
+        raw = (torch.sum(prob_sum * tokens_per_expert) * self.num_experts * sp_size
                / (self.topk * total * total))
         aux = raw * coeff
         self._metrics = {**(self._metrics or {}), "aux_loss": (aux / coeff).detach(),
                          "aux_loss_scaled": aux.detach()}
         return MoEAuxLossAutoScaler.apply(probs, aux)
 
-    def apply_z_loss(self, logits, padding_mask=None):
+    def apply_z_loss(self, logits, padding_mask=None, z_sum=None):
+        """``router.py:225-270``; the local z-loss is ``z_loss_func``'s mean of
+        the squared log-sum-exps, formed from their sum ``z_sum`` (computed here
+        through ``router_loss_stats`` when not given)."""
         coeff = self.config.moe_z_loss_coeff
         if not coeff or not (self.training and torch.is_grad_enabled()):
             return logits
+        if z_sum is None:
+            z_sum = ops.router_loss_stats(logits, self.topk, self.score_function, padding_mask,
+                                          aux=False, z=True)[2]
         if padding_mask is not None:
             local = (~padding_mask.reshape(-1).bool()).sum()
+            local_z = z_sum.to(logits.dtype) / torch.clamp(local, min=1)
         else:
             local = torch.tensor(logits.shape[0], device=logits.device, dtype=torch.long)
+            local_z = (z_sum / max(logits.shape[0], 1)).to(logits.dtype)
         total = local.clone()
         sp_size = _group_size(self.sp_group)
         if sp_size > 1:
             dist.all_reduce(total, op=dist.ReduceOp.SUM, group=self.sp_group)
-        z = z_loss_func(logits, coeff, padding_mask) * (sp_size * local / torch.clamp(total, min=1))
+        z = local_z * coeff * (sp_size * local / torch.clamp(total, min=1))
         self._metrics = {**(self._metrics or {}), "z_loss": (z / coeff).detach(),
                          "z_loss_scaled": z.detach()}
         return MoEAuxLossAutoScaler.apply(logits, z)
@@ -201,7 +216,17 @@ class TopKRouter(Router):
         input_ids = input_ids.view(-1) if input_ids is not None else None
         if self.use_hash_routing and input_ids is None:
             raise ValueError("Hash routing requires input_ids.")
-        logits = self.apply_z_loss(logits, padding_mask=padding_mask)
+        training = self.training and torch.is_grad_enabled()
+        want_z = bool(self.config.moe_z_loss_coeff) and training
+        want_aux = (training and not self.use_hash_routing
+                    and self.config.moe_aux_loss_coeff > 0.0)
+        stats = None
+        if want_z or want_aux:
+            # One pass over the logits for both losses (router.py:299, 319-334).
+            stats = ops.router_loss_stats(logits, self.topk, self.score_function, padding_mask,
+                                          aux=want_aux, z=want_z)
+        logits = self.apply_z_loss(logits, padding_mask=padding_mask,
+                                   z_sum=stats[2] if want_z else None)
         if self.routing_type != "none":
             raise ValueError(f"Unsupported MoE routing type: {self.routing_type}")
         probs, routing_map, expert_indices = ops.topk_softmax_with_capacity(
@@ -216,11 +241,8 @@ class TopKRouter(Router):
             hash_table=getattr(self, "tid2eid", None),
             input_ids=input_ids,
         )
-        if (self.training and torch.is_grad_enabled() and not self.use_hash_routing
-                and self.config.moe_aux_loss_coeff > 0.0):
-            aux_map, aux_scores = compute_routing_scores_for_aux_loss(
-                logits, self.topk, self.score_function, padding_mask)
-            probs = self._apply_aux_loss(probs, aux_scores, aux_map)
+        if want_aux:
+            probs = self._apply_aux_loss(probs, stats[0], stats[1])
         if self.enable_expert_bias and accumulate_tokens_per_expert and torch.is_grad_enabled():
             with torch.no_grad():
                 counts = mask_padding_tokens(routing_map, padding_mask).sum(dim=0).to(torch.float32)

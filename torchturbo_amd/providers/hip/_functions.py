@@ -96,6 +96,56 @@ class TopKRouting(torch.autograd.Function):
         return out, None, None, None, None, None, None, None, None
 
 
+class RouterLossStats(torch.autograd.Function):
+    """``(prob_sum [E] f32, tokens_per_expert [E] int64, z_sum [] f32)`` of the
+    router logits in one pass (``tt_router_loss_fwd``); the backward is one
+    pass too (``tt_router_loss_bwd``). Parts that are switched off come back
+    as zeros."""
+
+    @staticmethod
+    def forward(ctx, logits, topk, score_function, padding_mask, want_aux, want_z):
+        logits = logits.contiguous()
+        T, E = logits.shape
+        dev = logits.device
+        pad = None
+        if padding_mask is not None:
+            pad = padding_mask.reshape(-1).to(device=dev, dtype=torch.uint8).contiguous()
+            if pad.numel() != T:
+                raise ValueError(f"padding_mask has {pad.numel()} entries for {T} tokens")
+        sf = L.TT_SCORE[score_function]
+        if want_aux:
+            prob_sum = torch.empty((E,), dtype=torch.float32, device=dev)
+            counts = torch.empty((E,), dtype=torch.int64, device=dev)
+        else:
+            prob_sum = torch.zeros((E,), dtype=torch.float32, device=dev)
+            counts = torch.zeros((E,), dtype=torch.int64, device=dev)
+        z_sum = (torch.empty if want_z else torch.zeros)((), dtype=torch.float32, device=dev)
+        ws_bytes = L.router_loss_workspace(T, E)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+        L.call("tt_router_loss_fwd", L.ptr(logits), L.dtype_code(logits.dtype), T, E, int(topk), sf,
+               L.ptr(pad), L.ptr(prob_sum) if want_aux else None,
+               L.ptr(counts) if want_aux else None, L.ptr(z_sum) if want_z else None, L.ptr(ws),
+               ws_bytes, L.stream(dev))
+        ctx.save_for_backward(logits, pad)
+        ctx.sf = sf
+        ctx.mark_non_differentiable(counts)
+        ctx.set_materialize_grads(False)
+        return prob_sum, counts, z_sum
+
+    @staticmethod
+    def backward(ctx, g_prob_sum, _g_counts, g_z_sum):
+        if g_prob_sum is None and g_z_sum is None:
+            return None, None, None, None, None, None
+        logits, pad = ctx.saved_tensors
+        T, E = logits.shape
+        gp = None if g_prob_sum is None else g_prob_sum.to(torch.float32).contiguous()
+        gz = None if g_z_sum is None else g_z_sum.to(torch.float32).reshape(1).contiguous()
+        out = torch.empty_like(logits)
+        L.call("tt_router_loss_bwd", L.ptr(logits), L.dtype_code(logits.dtype), T, E, ctx.sf,
+               L.ptr(pad), L.ptr(gp), L.ptr(gz), L.ptr(out), L.stream(logits.device))
+        return out, None, None, None, None, None
+
+
 # ---------------------------------------------------------------------------
 # Permutation
 # ---------------------------------------------------------------------------

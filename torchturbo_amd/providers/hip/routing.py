@@ -13,7 +13,7 @@ from __future__ import annotations
 from ...dispatch import OpImpl, OpImplKind, register_op
 from ...runtime import TurboDevice
 from . import PRIORITY
-from ._functions import TopKRouting, require_cuda
+from ._functions import RouterLossStats, TopKRouting, require_cuda
 from .available import hip_available
 
 
@@ -39,3 +39,28 @@ class HipTopKSoftmax(OpImpl):
         bias = expert_bias if score_function != "softmax" or use_pre_softmax else None
         return TopKRouting.apply(logits, int(topk), score_function, bool(use_pre_softmax),
                                  num_groups, group_topk, scaling_factor, bias, fixed)
+
+
+@register_op(op_name="router_loss_stats", impl_name="hip_router_loss_stats",
+             kind=OpImplKind.CUSTOM, priority=PRIORITY, devices=(TurboDevice.CUDA,))
+class HipRouterLossStats(OpImpl):
+    """``(prob_sum [E], tokens_per_expert [E], z_sum [])``: the [T, E] sums of
+    the router's aux loss (``moe_utils.py:15-43``, ``router.py:164-209``) and
+    z-loss (``moe_utils.py:46-70``, ``router.py:225-270``) in one kernel pass
+    per direction, instead of the softmax / top-k / scatter / reductions of
+    the native composition."""
+
+    def available(self) -> bool:
+        return hip_available()
+
+    def __call__(self, logits, topk, score_function="softmax", padding_mask=None, *, aux=True,
+                 z=True):
+        require_cuda(logits)
+        if logits.dim() != 2:
+            raise ValueError(f"Expected 2D logits [num_tokens, num_experts], got {logits.dim()}.")
+        if score_function not in ("softmax", "sigmoid", "sqrtsoftplus"):
+            raise ValueError(f"Invalid score_function: {score_function}")
+        if aux and not 1 <= int(topk) <= logits.shape[1]:
+            raise ValueError(f"topk must be in [1, {logits.shape[1]}], got {topk}")
+        return RouterLossStats.apply(logits, int(topk), score_function, padding_mask, bool(aux),
+                                     bool(z))
