@@ -58,6 +58,23 @@ int tt_router_topk_bwd(const void* logits, int logits_dtype, int64_t num_tokens,
                        int32_t pre_softmax, float scaling_factor, const int64_t* top_indices,
                        const void* grad_probs, void* grad_logits, void* stream);
 
+/* Gating linear fused with tt_router_topk_fwd. Replaces TopKRouter.gating
+ * (models/modules/moe/router.py:25-58,84-101: linear(x.to(rdt), W.to(rdt)))
+ * followed by the top-k above, for one MoE layer's router.
+ * x [T, hidden] and weight [E, hidden] share in_dtype (bf16/f16); logits
+ * [T, E] are written in logits_dtype (f32, or in_dtype) as fp32 sums of the
+ * exact 16-bit products rounded once, then routed exactly as
+ * tt_router_topk_fwd routes logits of that dtype (same outputs and
+ * arguments). E in {32, 64, ..., 256}, hidden a multiple of 64, x and weight
+ * 16-byte aligned. The backward is tt_router_topk_bwd plus the two plain
+ * GEMMs of the linear. */
+int tt_router_gate_fwd(const void* x, const void* weight, int in_dtype, int64_t num_tokens,
+                       int64_t hidden, int32_t num_experts, int logits_dtype, int32_t topk,
+                       int32_t score_function, int32_t pre_softmax, const float* expert_bias,
+                       int32_t num_groups, int32_t group_topk, float scaling_factor,
+                       const int64_t* fixed_indices, void* logits, void* probs,
+                       uint8_t* routing_map, int64_t* top_indices, void* stream);
+
 /* ---- Router loss statistics (aux load-balancing loss, z-loss) ------------
  * Replaces the [T, E] work of compute_routing_scores_for_aux_loss and
  * z_loss_func (models/modules/moe/moe_utils.py:15-70) as used by

@@ -168,3 +168,24 @@ class TorchRouterLossStats(OpImpl):
     def __call__(self, logits, topk, score_function="softmax", padding_mask=None, *, aux=True,
                  z=True):
         return router_loss_stats(logits, topk, score_function, padding_mask, aux=aux, z=z)
+
+
+def router_gate_topk(x, weight, router_dtype, topk, **kwargs):
+    """``TopKRouter.gating`` (``router.py:25-58,84-101``: ``linear`` of the
+    inputs and the weight cast to the router dtype, autocast off) followed by
+    ``topk_softmax_with_capacity``; returns ``(probs, routing_map,
+    top_indices, logits)``."""
+    with torch.autocast(device_type=x.device.type, enabled=False):
+        logits = F.linear(x.to(router_dtype), weight.to(router_dtype))
+    logits2 = logits.reshape(-1, logits.shape[-1])
+    if kwargs.get("input_ids") is not None:
+        kwargs = {**kwargs, "input_ids": kwargs["input_ids"].reshape(-1)}
+    probs, routing_map, top = topk_softmax_with_capacity(logits2, topk, **kwargs)
+    return probs, routing_map, top, logits2
+
+
+@register_op(op_name="router_gate_topk", impl_name="torch_router_gate_topk",
+             kind=OpImplKind.NATIVE, priority=0, devices=())
+class TorchRouterGateTopK(OpImpl):
+    def __call__(self, x, weight, router_dtype, topk, **kwargs):
+        return router_gate_topk(x, weight, router_dtype, topk, **kwargs)

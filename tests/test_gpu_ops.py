@@ -133,6 +133,107 @@ def test_router_ties_go_to_lower_expert(hip_ops):
     assert ids.cpu().tolist() == [[1, 2]]
 
 
+# T, H, E, k, score, pre-softmax, groups, group_topk, scale, bias, input dtype, router dtype
+GATE_CASES = [
+    (1000, 2048, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16, torch.float32),
+    (333, 512, 256, 8, "sigmoid", False, 8, 4, 2.5, True, torch.bfloat16, torch.bfloat16),
+    (100, 64, 32, 2, "sqrtsoftplus", False, None, None, None, False, torch.bfloat16, torch.float32),
+    (65, 128, 160, 6, "softmax", True, None, None, 1.5, True, torch.float16, torch.float32),
+    (129, 192, 64, 4, "softmax", False, None, None, None, False, torch.bfloat16, torch.bfloat16),
+    (0, 256, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", GATE_CASES,
+                         ids=lambda c: f"T{c[0]}H{c[1]}E{c[2]}k{c[3]}{c[4]}{str(c[10])[6:]}-{str(c[11])[6:]}")
+def test_router_gate_topk_matches_linear_and_router(hip_ops, case):
+    """Fused gating linear + top-k (router.py:25-101, utils.py:127-230): logits
+    vs the exact-product fp32 linear of the same 16-bit inputs (the order of the
+    fp32 sum differs), then the oracle top-k applied to the kernel's own logits
+    (bit-exact ids and map), and gradients of x and the weight vs autograd."""
+    T, H, E, k, score, pre, groups, gtopk, scale, use_bias, idt, rdt = case
+    g = torch.Generator().manual_seed(T * 7 + E)
+    x = torch.randn(T, H, generator=g).to(idt)
+    w = (torch.randn(E, H, generator=g) * H ** -0.5).to(idt)
+    bias = (torch.randn(E, generator=g) * 0.05) if use_bias else None
+    kw = dict(use_pre_softmax=pre, num_groups=groups, group_topk=gtopk, scaling_factor=scale,
+              score_function=score, expert_bias=bias)
+    xd = x.to(DEV).requires_grad_()
+    wd = w.to(DEV).requires_grad_()
+    probs, rmap, ids, logits = hip_ops.router_gate_topk(
+        xd, wd, rdt, k, **{**kw, "expert_bias": None if bias is None else bias.to(DEV)})
+    assert logits.dtype == rdt and probs.dtype == rdt and logits.shape == (T, E)
+    exact = x.double() @ w.double().T
+    lg = logits.detach().cpu()
+    if rdt == torch.float32:
+        err = (lg.double() - exact).abs().max().item() if T else 0.0
+        assert err <= 1e-5 * max(1.0, exact.abs().max().item() if T else 1.0), err
+    else:  # one rounding of an fp32 sum: within one bf16 step of the exact value
+        assert torch.all((lg.double() - exact).abs() <= exact.abs() * 2 ** -8 + 1e-6)
+    ref_lg = lg.clone().requires_grad_()
+    pr, mr, ir = o_route.topk_softmax_with_capacity(ref_lg, k, **kw)
+    if rdt == torch.float32:
+        assert torch.equal(ids.cpu(), ir) and torch.equal(rmap.cpu(), mr)
+        rows = slice(None)
+    else:
+        # bf16 logits tie; PyTorch's topk has no tie rule (the kernel takes the
+        # lower id): compare the selected sets where the k-th and (k+1)-th
+        # logits differ, as test_router_matches_oracle does
+        srt = lg.float().sort(dim=1, descending=True).values
+        rows = srt[:, k - 1] != srt[:, k]
+        assert torch.equal(rmap.cpu()[rows], mr[rows])
+        assert torch.equal(ids.cpu()[rows].sort(1).values, ir[rows].sort(1).values)
+    tol = 2e-6 if rdt == torch.float32 else 8e-3
+    if T:
+        assert rel_errors(probs.detach().cpu()[rows], pr.detach()[rows])[0] <= tol
+    # backward through probs and logits; the linear's backward as the reference forms it
+    gp = torch.randn(T, E, generator=g).to(rdt)
+    gl = torch.randn(T, E, generator=g).to(rdt)
+    xr = x.clone().requires_grad_()
+    wr = w.clone().requires_grad_()
+    ((pr * gp).sum() + (ref_lg * gl).sum()).backward()
+    glog = ref_lg.grad  # d loss / d logits of the reference composition
+    gx_r = (glog.to(rdt) @ wr.detach().to(rdt)).to(idt)
+    gw_r = (glog.to(rdt).T @ xr.detach().to(rdt)).to(idt)
+    ((probs * gp.to(DEV)).sum() + (logits * gl.to(DEV)).sum()).backward()
+    if T == 0:
+        assert xd.grad.shape == (0, H)
+        return
+    if rdt != torch.float32 and not bool(rows.all()):
+        return  # a tie row routes differently, so its gradient differs; selection checked above
+    assert_bf16_close(xd.grad.cpu(), gx_r, what="dx")
+    assert_bf16_close(wd.grad.cpu(), gw_r, what="dw")
+
+
+def test_router_gate_topk_hash_routing(hip_ops):
+    T, H, E, k = 40, 128, 64, 4
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(T, H, generator=g).bfloat16()
+    w = (torch.randn(E, H, generator=g) * 0.1).bfloat16()
+    table = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(10)])
+    input_ids = torch.randint(0, 10, (T,), generator=g)
+    kw = dict(use_pre_softmax=True, score_function="sigmoid", use_hash_routing=True,
+              scaling_factor=1.7)
+    p, m, i, lg = hip_ops.router_gate_topk(x.to(DEV), w.to(DEV), torch.float32, k,
+                                           hash_table=table.to(DEV), input_ids=input_ids.to(DEV),
+                                           **kw)
+    pr, mr, ir = o_route.topk_softmax_with_capacity(lg.cpu(), k, hash_table=table,
+                                                    input_ids=input_ids, **kw)
+    assert torch.equal(i.cpu(), ir) and torch.equal(m.cpu(), mr)
+    assert rel_errors(p.cpu(), pr)[0] <= 2e-6
+
+
+def test_router_gate_rejects_unsupported_shapes(hip_ops):
+    x = torch.randn(8, 96, device=DEV).bfloat16()
+    w = torch.randn(64, 96, device=DEV).bfloat16()
+    with pytest.raises(ValueError, match="multiple of 64"):
+        hip_ops.router_gate_topk(x, w, torch.float32, 2)
+    x = torch.randn(8, 128, device=DEV).bfloat16()
+    w = torch.randn(48, 128, device=DEV).bfloat16()
+    with pytest.raises(ValueError, match="multiple of 32"):
+        hip_ops.router_gate_topk(x, w, torch.float32, 2)
+
+
 # T, E, k, score function, logits dtype, padded rows
 LOSS_CASES = [
     (1000, 128, 8, "softmax", torch.float32, False),

@@ -15,6 +15,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.native_providers.routing import router_loss_stats
+from tests.conftest import assert_bf16_close
 from torchturbo_amd.dispatch import OpPolicy
 from torchturbo_amd.moe import MoEConfig, TopKRouter
 from torchturbo_amd.moe.router import MoEAuxLossAutoScaler
@@ -174,3 +175,43 @@ def test_oracle_loss_stats_switches_and_padding_invariants():
     parts = [router_loss_stats(logits[i:i + 1], 3, "softmax") for i in range(7)]
     for j, whole in enumerate((ps, cn, zs)):
         torch.testing.assert_close(sum(p[j] for p in parts), whole)
+
+
+@pytest.mark.parametrize("rdt", [None, "fp32"])
+def test_fused_gate_path_equals_reference_composition(cpu_ops, rdt):
+    """bf16 router weight, E a multiple of 32: forward takes the fused
+    gating + top-k op; its outputs, losses and gradients equal the reference
+    composition (gating, then routing) run on the same module."""
+    torch.manual_seed(6)
+    cfg = MoEConfig(hidden_size=64, num_moe_experts=64, moe_router_topk=4,
+                    moe_router_dtype=rdt, moe_aux_loss_coeff=0.01, moe_z_loss_coeff=0.002,
+                    params_dtype=torch.bfloat16)
+    router = TopKRouter(cfg)
+    torch.nn.init.normal_(router.weight, std=0.1)
+    x = torch.randn(3, 5, 64).bfloat16()
+    assert router._can_fuse_gate(x)
+    w = torch.randn(15, 64)
+
+    def run(fused):
+        router.weight.grad = None
+        xi = x.clone().requires_grad_()
+        if fused:
+            probs, rmap, ids, logits = router(xi)
+        else:
+            logits = router.gating(xi)
+            probs, rmap, ids = router.routing(logits)
+        ((probs.float() * w).sum() + logits.float().square().sum() * 1e-3).backward()
+        return probs, rmap, ids, logits, xi.grad, router.weight.grad.clone(), router.pop_metrics()
+
+    a, b = run(True), run(False)
+    for u, v in zip(a[:4], b[:4]):  # probs, map, ids, logits: the same ops
+        assert torch.equal(u, v)
+    for key in ("aux_loss", "z_loss"):
+        torch.testing.assert_close(a[6][key], b[6][key], rtol=0, atol=0)
+    # autograd adds the logits' gradient terms in another order: in a bf16
+    # router dtype that moves the last bit of some sums
+    for u, v in zip(a[4:6], b[4:6]):
+        if rdt is None:
+            assert_bf16_close(u, v)
+        else:
+            torch.testing.assert_close(u, v)

@@ -35,6 +35,8 @@ _PROTOS: dict[str, list] = {
     "tt_router_topk_fwd": [P, c_int, I64, I32, I32, I32, I32, P, I32, I32, c_float, P, P, P, P, P],
     "tt_router_topk_bwd": [P, c_int, I64, I32, I32, I32, I32, c_float, P, P, P, P],
     "tt_route_index_workspace": [I64, I32],
+    "tt_router_gate_fwd": [P, P, c_int, I64, I64, I32, c_int, I32, I32, I32, P, I32, I32, c_float,
+                           P, P, P, P, P, P],
     "tt_router_loss_workspace": [I64, I32],
     "tt_router_loss_fwd": [P, c_int, I64, I32, I32, I32, P, P, P, P, P, c_size_t, P],
     "tt_router_loss_bwd": [P, c_int, I64, I32, I32, P, P, P, P, P],

@@ -67,25 +67,17 @@ __device__ __forceinline__ float softplus_f(float x) {
   return x > 20.0f ? x : log1pf(expf(x));
 }
 
+// Top-k routing of token t by one wave from its logits (fp32 values of the
+// logits dtype ldt; lane l holds experts l*EPL .. l*EPL + EPL - 1, -inf past
+// E): scores, selection, probabilities, and the outputs of row t.
 template <int EPL>
-__global__ __launch_bounds__(256) void router_fwd_kernel(
-    const void* __restrict__ logits, int ldt, int64_t T, int E, int K, int score_fn,
-    int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
+__device__ __forceinline__ void route_row(
+    int lane, int64_t t, const float (&lg)[EPL], const bool (&valid)[EPL], int ldt, int E, int K,
+    int score_fn, int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
     const int64_t* __restrict__ fixed, void* __restrict__ probs, uint8_t* __restrict__ rmap,
     int64_t* __restrict__ top_idx) {
-  const int lane = lane_id();
-  const int64_t t = (int64_t)blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-  if (t >= T) return;  // whole wave; no block-level synchronisation below
   const float NEG = -INFINITY;
-
-  float lg[EPL], sc[EPL], sel[EPL];
-  bool valid[EPL];
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int e = lane * EPL + i;
-    valid[i] = e < E;
-    lg[i] = valid[i] ? load_as_f32(logits, ldt, t * E + e) : NEG;
-  }
+  float sc[EPL], sel[EPL];
 
   // Scores.
   if (score_fn == TT_SCORE_SOFTMAX) {
@@ -292,6 +284,27 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
       rmap[o] = taken[i] ? 1 : 0;
     }
   }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void router_fwd_kernel(
+    const void* __restrict__ logits, int ldt, int64_t T, int E, int K, int score_fn,
+    int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
+    const int64_t* __restrict__ fixed, void* __restrict__ probs, uint8_t* __restrict__ rmap,
+    int64_t* __restrict__ top_idx) {
+  const int lane = lane_id();
+  const int64_t t = (int64_t)blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole wave; no block-level synchronisation below
+  float lg[EPL];
+  bool valid[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane * EPL + i;
+    valid[i] = e < E;
+    lg[i] = valid[i] ? load_as_f32(logits, ldt, t * E + e) : -INFINITY;
+  }
+  route_row<EPL>(lane, t, lg, valid, ldt, E, K, score_fn, pre_softmax, bias, G, GK, scaling,
+                 fixed, probs, rmap, top_idx);
 }
 
 template <int EPL>
@@ -894,6 +907,232 @@ void launch_router_bwd(dim3 g, hipStream_t s, const void* logits, int ldt, int64
                      scale, top, grad, gl);
 }
 
+// ---------------------------------------------------------------------------
+// Gating linear fused with the top-k (models/modules/moe/router.py:25-58, then
+// utils.py:127-230): logits = x W^T for a tile of 64 tokens and all E experts
+// on MFMA (16-bit operands, fp32 accumulation), rounded to the logits dtype,
+// written out, and routed from LDS by route_row (one wave per token). With
+// 16-bit x and W the reference's fp32 router (x.float() @ W.float().T) forms
+// the same exact products; only the order of the fp32 sum differs.
+// Operand rows (64 tokens, then E experts) stream HBM -> LDS by buffer DMA in
+// 64-deep chunks, 128-byte rows, chunk c of row r in slot c ^ ((r >> 1) & 7);
+// rows past T come back as zeros from the resource bound. Template P = DMA
+// instructions per wave per chunk = (64 + E) / 32, so E = 32 P - 64.
+// ---------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(4))) int gi32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 gbf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 gf16x8;
+typedef __attribute__((ext_vector_type(16))) float gf32x16;
+typedef __attribute__((ext_vector_type(4))) unsigned gu32x4;
+typedef __attribute__((address_space(3))) char glds_char;
+typedef __attribute__((address_space(3))) gu32x4 glds_u32x4;
+
+constexpr int kGateTokens = 64;
+constexpr int kGateRow = 128;  // bytes of one row of a 64-deep chunk
+
+#define RG_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8))
+
+__device__ __forceinline__ gi32x4 rg_rsrc(const void* base, int64_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t n = bytes <= 0 ? 0u : (bytes < 0xFFFFFFF0ll ? (uint32_t)bytes : 0xFFFFFFF0u);
+  gi32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(b >> 32) & 0xFFFFu));
+  r.z = __builtin_amdgcn_readfirstlane((int)n);
+  r.w = 0x00020000;
+  return r;
+}
+
+// One 16-byte load per lane into LDS at lds_addr + 16 * lane (lds_addr -> M0).
+__device__ __forceinline__ void rg_dma16(uint32_t voff, gi32x4 rsrc, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t rg_swz(int r, int c) {
+  return (uint32_t)(r * kGateRow + ((c ^ ((r >> 1) & 7)) << 4));
+}
+
+template <int ET>
+__device__ __forceinline__ gf32x16 rg_mma(const uint4& a, const uint4& b, const gf32x16& c);
+template <>
+__device__ __forceinline__ gf32x16 rg_mma<TT_BF16>(const uint4& a, const uint4& b,
+                                                   const gf32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gbf16x8, a),
+                                                  __builtin_bit_cast(gbf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ gf32x16 rg_mma<TT_F16>(const uint4& a, const uint4& b,
+                                                  const gf32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(gf16x8, a),
+                                                 __builtin_bit_cast(gf16x8, b), c, 0, 0, 0);
+}
+
+template <int P>
+struct GateShape {
+  static constexpr int E = 32 * P - 64;                    // experts
+  static constexpr int NT = E / 32;                         // 32-expert tiles
+  static constexpr int WAVES = 16;                          // waves per block
+  static constexpr int TPW = (2 * NT + WAVES - 1) / WAVES;  // 32x32 output tiles per wave
+  static constexpr int NI = 4 * P;                          // DMA loads per chunk (8 rows each)
+  static constexpr int PW = (NI + WAVES - 1) / WAVES;       // ... per wave (the rest: dummy)
+  static constexpr int SB = (kGateTokens + E) * kGateRow;   // stage bytes
+  static constexpr int NS = 4 * SB + 1024 <= 128 * 1024 ? 4 : 3;  // stages in the ring
+  static constexpr int LS = E + 4;                          // logits tile row stride (floats)
+  static constexpr int EPL = E <= 64 ? 1 : (E <= 128 ? 2 : 4);
+  static constexpr int RING = NS * SB + 1024;               // + a dummy DMA target
+  static constexpr int LDS = RING > kGateTokens * LS * 4 ? RING : kGateTokens * LS * 4;
+};
+
+// 16 waves: the GEMM gives each wave one or two 32x32 (token, expert) tiles;
+// the selection then routes 4 tokens per wave.
+template <int ET, int P>
+__global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
+    const char* __restrict__ x, const char* __restrict__ w, int64_t T, int H, int ldt, int K,
+    int score_fn, int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
+    const int64_t* __restrict__ fixed, void* __restrict__ logits, void* __restrict__ probs,
+    uint8_t* __restrict__ rmap, int64_t* __restrict__ top_idx) {
+  typedef GateShape<P> S;
+  constexpr int E = S::E, NS = S::NS, SB = S::SB, EPL = S::EPL, PW = S::PW;
+  extern __shared__ __align__(16) char gsm[];
+  glds_char* const lds = (glds_char*)gsm;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t t0 = (int64_t)blockIdx.x * kGateTokens;
+  const int nch = H / 64;
+  const int64_t nrow = T - t0 < kGateTokens ? T - t0 : kGateTokens;
+  const gi32x4 rx = rg_rsrc(x + t0 * H * 2, nrow * H * 2);
+  const gi32x4 rw = rg_rsrc(w, (int64_t)E * H * 2);
+
+  // This wave's PW loads of chunk kc: load g = PW wave + q fills stage rows
+  // 8 g .. 8 g + 7. Loads past the NI of a chunk, and chunks past the end,
+  // read a zero-size resource (loads g >= NI into the dummy slot), so every
+  // wave always has PW loads per chunk in flight and the counts below hold.
+  auto issue = [&](int kc, int stage) {
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+      const int g = wave * PW + q;
+      const bool real = g < S::NI;
+      const bool isx = 8 * g < kGateTokens;
+      const int r = 8 * g + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int orow = isx ? r : r - kGateTokens;
+      const uint32_t off = (uint32_t)(((int64_t)orow * H + (int64_t)kc * 64 + c * 8) * 2);
+      const bool live = real && kc < nch;
+      gi32x4 rs;
+      rs.x = __builtin_amdgcn_readfirstlane(isx ? rx.x : rw.x);
+      rs.y = __builtin_amdgcn_readfirstlane(isx ? rx.y : rw.y);
+      rs.z = __builtin_amdgcn_readfirstlane(live ? (isx ? rx.z : rw.z) : 0);
+      rs.w = 0x00020000;
+      const uint32_t dst = real ? (uint32_t)(stage * SB + 8 * g * kGateRow) : (uint32_t)(NS * SB);
+      rg_dma16(live ? off : 0u, rs, lds0 + dst);
+    }
+  };
+
+  gf32x16 acc[S::TPW];
+#pragma unroll
+  for (int i = 0; i < S::TPW; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s, s);
+  for (int kc = 0; kc < nch; ++kc) {
+    RG_WAIT_VMCNT((NS - 2) * PW);  // this wave's part of chunk kc has landed
+    __syncthreads();               // everyone's part has; stage (kc - 1) % NS is free
+    issue(kc + NS - 1, (kc + NS - 1) % NS);
+    glds_char* const st = lds + (kc % NS) * SB;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = 2 * s + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < S::TPW; ++i) {
+        const int tile = wave + S::WAVES * i;  // token tile tile & 1, expert tile tile >> 1
+        if (tile < 2 * S::NT) {
+          const uint4 a = __builtin_bit_cast(uint4, *reinterpret_cast<const glds_u32x4*>(
+                                                        st + rg_swz(32 * (tile & 1) + (lane & 31), c)));
+          const uint4 b = __builtin_bit_cast(
+              uint4, *reinterpret_cast<const glds_u32x4*>(
+                         st + rg_swz(kGateTokens + 32 * (tile >> 1) + (lane & 31), c)));
+          acc[i] = rg_mma<ET>(b, a, acc[i]);
+        }
+      }
+    }
+  }
+  RG_WAIT_VMCNT(0);
+  __syncthreads();
+
+  // Logits tile in LDS (fp32 values of the logits dtype). Lane l holds token
+  // row 32 m + l % 32, experts 32 j + 8 q + 4 (l / 32) + 0..3 in acc[4 q ..].
+  float* const L = reinterpret_cast<float*>(gsm);
+#pragma unroll
+  for (int i = 0; i < S::TPW; ++i) {
+    const int tile = wave + S::WAVES * i;
+    if (tile >= 2 * S::NT) continue;
+    const int row = 32 * (tile & 1) + (lane & 31);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = 32 * (tile >> 1) + 8 * q + 4 * (lane >> 5);
+      float4 v;
+      v.x = round_to(acc[i][4 * q + 0], ldt);
+      v.y = round_to(acc[i][4 * q + 1], ldt);
+      v.z = round_to(acc[i][4 * q + 2], ldt);
+      v.w = round_to(acc[i][4 * q + 3], ldt);
+      *reinterpret_cast<float4*>(L + row * S::LS + col) = v;
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kGateTokens * E; idx += 64 * S::WAVES) {
+    const int row = idx / E, col = idx % E;
+    if (row < nrow) store_from_f32(logits, ldt, (t0 + row) * E + col, L[row * S::LS + col]);
+  }
+  constexpr int RPW = kGateTokens / S::WAVES;  // tokens routed per wave
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int row = wave * RPW + rr;
+    if (row >= nrow) break;  // wave-uniform; no block synchronisation follows
+    float lg[EPL];
+    bool valid[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane * EPL + i;
+      valid[i] = e < E;
+      lg[i] = valid[i] ? L[row * S::LS + e] : -INFINITY;
+    }
+    route_row<EPL>(lane, t0 + row, lg, valid, ldt, E, K, score_fn, pre_softmax, bias, G, GK,
+                   scaling, fixed, probs, rmap, top_idx);
+  }
+}
+
+template <int ET, int P>
+int launch_gate(const void* x, const void* w, int64_t T, int H, int ldt, int K, int sf, int pre,
+                const float* bias, int G, int GK, float scale, const int64_t* fixed, void* logits,
+                void* probs, uint8_t* rmap, int64_t* top, hipStream_t s) {
+  typedef GateShape<P> S;
+  static_assert(S::LDS <= 160 * 1024, "gate tile exceeds LDS");
+  static bool allowed = false;  // the attribute belongs to the kernel, for every device
+  if (!allowed) {
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&router_gate_fwd_kernel<ET, P>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      tt_set_error("router_gate: hipFuncSetAttribute(%d bytes): %s", S::LDS,
+                   hipGetErrorString(e));
+      return TT_ERR_HIP;
+    }
+    allowed = true;
+  }
+  const dim3 grid((unsigned)((T + kGateTokens - 1) / kGateTokens));
+  hipLaunchKernelGGL((router_gate_fwd_kernel<ET, P>), grid, dim3(64 * S::WAVES), S::LDS, s,
+                     static_cast<const char*>(x), static_cast<const char*>(w), T, H, ldt, K, sf,
+                     pre, bias, G, GK, scale, fixed, logits, probs, rmap, top);
+  return tt_check_launch("router_gate_fwd");
+}
+
 int epl_for(int E) {
   const int need = (E + TT_WAVE - 1) / TT_WAVE;
   int epl = 1;
@@ -1110,4 +1349,85 @@ extern "C" int tt_router_loss_bwd(const void* logits, int logits_dtype, int64_t 
       return TT_ERR_UNSUPPORTED;
   }
   return tt_check_launch("router_loss_bwd");
+}
+
+extern "C" int tt_router_gate_fwd(const void* x, const void* weight, int in_dtype,
+                                  int64_t num_tokens, int64_t hidden, int32_t num_experts,
+                                  int logits_dtype, int32_t topk, int32_t score_function,
+                                  int32_t pre_softmax, const float* expert_bias,
+                                  int32_t num_groups, int32_t group_topk, float scaling_factor,
+                                  const int64_t* fixed_indices, void* logits, void* probs,
+                                  uint8_t* routing_map, int64_t* top_indices, void* stream) {
+  TT_REQUIRE(in_dtype == TT_BF16 || in_dtype == TT_F16,
+             "router_gate: input and weight must be bf16 or f16 (got dtype %d)", in_dtype);
+  TT_REQUIRE(logits_dtype == TT_F32 || logits_dtype == in_dtype,
+             "router_gate: logits dtype must be f32 or the input dtype");
+  TT_REQUIRE(num_tokens >= 0, "router_gate: negative token count");
+  TT_REQUIRE(hidden >= 64 && hidden % 64 == 0 && hidden <= (1 << 24),
+             "router_gate: hidden size must be a positive multiple of 64");
+  TT_REQUIRE(num_experts >= 32 && num_experts <= 256 && num_experts % 32 == 0,
+             "router_gate: num_experts must be a multiple of 32 in [32, 256]");
+  TT_REQUIRE(topk >= 1 && topk <= 64 && topk <= num_experts, "router_gate: bad topk");
+  TT_REQUIRE(score_function >= 0 && score_function <= 2, "router_gate: bad score function");
+  TT_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) == 0,
+             "router_gate: x and weight must be 16-byte aligned");
+  const int epl = epl_for(num_experts);
+  if (group_topk > 0 && fixed_indices == nullptr) {
+    TT_REQUIRE(num_groups > 0 && num_experts % num_groups == 0,
+               "router_gate: num_experts must be divisible by num_groups");
+    TT_REQUIRE(group_topk <= num_groups && topk % group_topk == 0,
+               "router_gate: topk must be divisible by group_topk <= num_groups");
+    const int gs = num_experts / num_groups;
+    const int width = gs / epl;
+    TT_REQUIRE(gs % epl == 0 && width >= 1 && (width & (width - 1)) == 0 && TT_WAVE % width == 0,
+               "router_gate: group size %d does not map onto whole lanes (%d experts per lane)",
+               gs, epl);
+    TT_REQUIRE(topk / group_topk <= gs, "router_gate: topk / group_topk exceeds the group size");
+    TT_REQUIRE(topk <= group_topk * gs, "router_gate: topk exceeds the experts of the kept groups");
+  }
+  if (num_tokens == 0) return TT_OK;
+  const int gk = fixed_indices ? 0 : group_topk;
+  const int H = (int)hidden;
+  const int P = (num_experts + 64) / 32;
+#define TT_GATE(ET)                                                                          \
+  switch (P) {                                                                               \
+    case 3: return launch_gate<ET, 3>(x, weight, num_tokens, H, logits_dtype, topk,          \
+                                      score_function, pre_softmax, expert_bias, num_groups,  \
+                                      gk, scaling_factor, fixed_indices, logits, probs,      \
+                                      routing_map, top_indices, S(stream));                  \
+    case 4: return launch_gate<ET, 4>(x, weight, num_tokens, H, logits_dtype, topk,          \
+                                      score_function, pre_softmax, expert_bias, num_groups,  \
+                                      gk, scaling_factor, fixed_indices, logits, probs,      \
+                                      routing_map, top_indices, S(stream));                  \
+    case 5: return launch_gate<ET, 5>(x, weight, num_tokens, H, logits_dtype, topk,          \
+                                      score_function, pre_softmax, expert_bias, num_groups,  \
+                                      gk, scaling_factor, fixed_indices, logits, probs,      \
+                                      routing_map, top_indices, S(stream));                  \
+    case 6: return launch_gate<ET, 6>(x, weight, num_tokens, H, logits_dtype, topk,          \
+                                      score_function, pre_softmax, expert_bias, num_groups,  \
+                                      gk, scaling_factor, fixed_indices, logits, probs,      \
+                                      routing_map, top_indices, S(stream));                  \
+    case 7: return launch_gate<ET, 7>(x, weight, num_tokens, H, logits_dtype, topk,          \
+                                      score_function, pre_softmax, expert_bias, num_groups,  \
+                                      gk, scaling_factor, fixed_indices, logits, probs,      \
+                                      routing_map, top_indices, S(stream));                  \
+    case 8: return launch_gate<ET, 8>(x, weight, num_tokens, H, logits_dtype, topk,          \
+                                      score_function, pre_softmax, expert_bias, num_groups,  \
+                                      gk, scaling_factor, fixed_indices, logits, probs,      \
+                                      routing_map, top_indices, S(stream));                  \
+    case 9: return launch_gate<ET, 9>(x, weight, num_tokens, H, logits_dtype, topk,          \
+                                      score_function, pre_softmax, expert_bias, num_groups,  \
+                                      gk, scaling_factor, fixed_indices, logits, probs,      \
+                                      routing_map, top_indices, S(stream));                  \
+    default: return launch_gate<ET, 10>(x, weight, num_tokens, H, logits_dtype, topk,        \
+                                        score_function, pre_softmax, expert_bias, num_groups, \
+                                        gk, scaling_factor, fixed_indices, logits, probs,     \
+                                        routing_map, top_indices, S(stream));                 \
+  }
+  if (in_dtype == TT_BF16) {
+    TT_GATE(TT_BF16)
+  } else {
+    TT_GATE(TT_F16)
+  }
+#undef TT_GATE
 }

@@ -12,6 +12,14 @@ kernel for each per direction. The scalar formulas on top of those sums, the
 sequence-parallel all-reduce and the metrics are the reference's
 (``router.py:164-270``). ``compute_routing_scores_for_aux_loss`` and
 ``z_loss_func`` (``moe_utils.py:15-70``) remain importable.
+
+``forward`` runs the gating linear and the top-k as one op
+(``router_gate_topk``: one HIP kernel on the GPU) when the inputs and the
+router weight share a 16-bit dtype, the router dtype is that dtype or fp32,
+E is a multiple of 32 up to 256 and the hidden size a multiple of 64; the
+z-loss is then attached to the probabilities instead of the logits the
+top-k read (the same gradients: the loss scaler is an identity). Other
+configurations run ``gating`` and ``routing`` as the reference does.
 """
 
 from __future__ import annotations
@@ -23,6 +31,17 @@ import torch.distributed as dist
 
 from ..dispatch import ops
 from .moe_config import MoEConfig
+
+
+def _op_resolves(name: str) -> bool:
+    """Whether the process dispatcher has an implementation of ``name`` for its device."""
+    from ..dispatch.ops import get_ops
+
+    try:
+        d = get_ops()
+    except RuntimeError:
+        return False
+    return bool(d.registry.list(lambda s: s.op_name == name)) and name not in d.unresolved_ops
 
 
 def _group_size(group) -> int:
@@ -184,9 +203,13 @@ class TopKRouter(Router):
         """``router.py:225-270``; the local z-loss is ``z_loss_func``'s mean of
         the squared log-sum-exps, formed from their sum ``z_sum`` (computed here
         through ``router_loss_stats`` when not given)."""
-        coeff = self.config.moe_z_loss_coeff
-        if not coeff or not (self.training and torch.is_grad_enabled()):
+        if not self.config.moe_z_loss_coeff or not (self.training and torch.is_grad_enabled()):
             return logits
+        return MoEAuxLossAutoScaler.apply(logits, self._z_loss(logits, padding_mask, z_sum))
+
+    def _z_loss(self, logits, padding_mask, z_sum=None):
+        """The scaled z-loss of ``router.py:239-264`` (metrics recorded)."""
+        coeff = self.config.moe_z_loss_coeff
         if z_sum is None:
             z_sum = ops.router_loss_stats(logits, self.topk, self.score_function, padding_mask,
                                           aux=False, z=True)[2]
@@ -203,34 +226,15 @@ class TopKRouter(Router):
         z = local_z * coeff * (sp_size * local / torch.clamp(total, min=1))
         self._metrics = {**(self._metrics or {}), "z_loss": (z / coeff).detach(),
                          "z_loss_scaled": z.detach()}
-        return MoEAuxLossAutoScaler.apply(logits, z)
+        return z
 
     def pop_metrics(self):
         metrics = self._metrics or {}
         self._metrics = None
         return metrics
 
-    def routing(self, logits, input_ids=None, padding_mask=None,
-                accumulate_tokens_per_expert: bool = True):
-        logits = logits.view(-1, self.config.num_moe_experts)
-        input_ids = input_ids.view(-1) if input_ids is not None else None
-        if self.use_hash_routing and input_ids is None:
-            raise ValueError("Hash routing requires input_ids.")
-        training = self.training and torch.is_grad_enabled()
-        want_z = bool(self.config.moe_z_loss_coeff) and training
-        want_aux = (training and not self.use_hash_routing
-                    and self.config.moe_aux_loss_coeff > 0.0)
-        stats = None
-        if want_z or want_aux:
-            # One pass over the logits for both losses (router.py:299, 319-334).
-            stats = ops.router_loss_stats(logits, self.topk, self.score_function, padding_mask,
-                                          aux=want_aux, z=want_z)
-        logits = self.apply_z_loss(logits, padding_mask=padding_mask,
-                                   z_sum=stats[2] if want_z else None)
-        if self.routing_type != "none":
-            raise ValueError(f"Unsupported MoE routing type: {self.routing_type}")
-        probs, routing_map, expert_indices = ops.topk_softmax_with_capacity(
-            logits, self.topk,
+    def _routing_kwargs(self, input_ids):
+        return dict(
             use_pre_softmax=self.config.moe_router_pre_softmax,
             num_groups=self.config.moe_router_num_groups,
             group_topk=self.config.moe_router_group_topk,
@@ -241,6 +245,23 @@ class TopKRouter(Router):
             hash_table=getattr(self, "tid2eid", None),
             input_ids=input_ids,
         )
+
+    def _loss_stats(self, logits, padding_mask):
+        """Which losses apply (``router.py:232-236,320-325``) and their sums,
+        from one pass over the logits (``router_loss_stats``)."""
+        training = self.training and torch.is_grad_enabled()
+        want_z = bool(self.config.moe_z_loss_coeff) and training
+        want_aux = (training and not self.use_hash_routing
+                    and self.config.moe_aux_loss_coeff > 0.0)
+        stats = None
+        if want_z or want_aux:
+            stats = ops.router_loss_stats(logits, self.topk, self.score_function, padding_mask,
+                                          aux=want_aux, z=want_z)
+        return want_z, want_aux, stats
+
+    def _finish_routing(self, probs, routing_map, want_aux, stats, padding_mask,
+                        accumulate_tokens_per_expert):
+        """Aux loss and expert-bias token counts (``router.py:319-354``)."""
         if want_aux:
             probs = self._apply_aux_loss(probs, stats[0], stats[1])
         if self.enable_expert_bias and accumulate_tokens_per_expert and torch.is_grad_enabled():
@@ -250,12 +271,56 @@ class TopKRouter(Router):
                     self.register_buffer("local_tokens_per_expert", torch.zeros_like(counts),
                                          persistent=False)
                 self.local_tokens_per_expert.add_(counts)
+        return probs
+
+    def routing(self, logits, input_ids=None, padding_mask=None,
+                accumulate_tokens_per_expert: bool = True):
+        logits = logits.view(-1, self.config.num_moe_experts)
+        input_ids = input_ids.view(-1) if input_ids is not None else None
+        if self.use_hash_routing and input_ids is None:
+            raise ValueError("Hash routing requires input_ids.")
+        # One pass over the logits for both losses (router.py:299, 319-334).
+        want_z, want_aux, stats = self._loss_stats(logits, padding_mask)
+        logits = self.apply_z_loss(logits, padding_mask=padding_mask,
+                                   z_sum=stats[2] if want_z else None)
+        if self.routing_type != "none":
+            raise ValueError(f"Unsupported MoE routing type: {self.routing_type}")
+        probs, routing_map, expert_indices = ops.topk_softmax_with_capacity(
+            logits, self.topk, **self._routing_kwargs(input_ids))
+        probs = self._finish_routing(probs, routing_map, want_aux, stats, padding_mask,
+                                     accumulate_tokens_per_expert)
         return probs, routing_map, expert_indices
+
+    def _can_fuse_gate(self, input) -> bool:
+        E = self.config.num_moe_experts
+        return (self.routing_type == "none"
+                and input.dtype in (torch.bfloat16, torch.float16)
+                and self.weight.dtype == input.dtype
+                and self.router_dtype(input.dtype) in (input.dtype, torch.float32)
+                and E % 32 == 0 and 32 <= E <= 256 and input.shape[-1] % 64 == 0
+                and _op_resolves("router_gate_topk"))
 
     def forward(self, input, input_ids=None, padding_mask=None,
                 accumulate_tokens_per_expert: bool = True):
         self._maintain_float32_expert_bias()
-        logits = self.gating(input)
-        probs, routing_map, expert_indices = self.routing(
-            logits, input_ids, padding_mask, accumulate_tokens_per_expert)
-        return probs, routing_map, expert_indices, logits
+        if not self._can_fuse_gate(input):
+            logits = self.gating(input)
+            probs, routing_map, expert_indices = self.routing(
+                logits, input_ids, padding_mask, accumulate_tokens_per_expert)
+            return probs, routing_map, expert_indices, logits
+        # gating (router.py:84-101) and top-k (router.py:277-317) as one op
+        ids = input_ids.view(-1) if input_ids is not None else None
+        if self.use_hash_routing and ids is None:
+            raise ValueError("Hash routing requires input_ids.")
+        if self.weight.device != input.device:
+            self.weight.data = self.weight.data.to(device=input.device)
+        probs, routing_map, expert_indices, logits = ops.router_gate_topk(
+            input, self.weight, self.router_dtype(input.dtype), self.topk,
+            **self._routing_kwargs(ids))
+        want_z, want_aux, stats = self._loss_stats(logits, padding_mask)
+        if want_z:
+            probs = MoEAuxLossAutoScaler.apply(
+                probs, self._z_loss(logits, padding_mask, stats[2]))
+        probs = self._finish_routing(probs, routing_map, want_aux, stats, padding_mask,
+                                     accumulate_tokens_per_expert)
+        return probs, routing_map, expert_indices, logits.view(*input.shape[:-1], -1)

@@ -87,13 +87,73 @@ class TopKRouting(torch.autograd.Function):
         if grad_probs is None:
             return None, None, None, None, None, None, None, None, None
         logits, top = ctx.saved_tensors
-        topk, sf, pre, scale = ctx.cfg
-        T, E = logits.shape
-        grad = grad_probs.to(logits.dtype).contiguous()
-        out = torch.empty_like(logits)
-        L.call("tt_router_topk_bwd", L.ptr(logits), L.dtype_code(logits.dtype), T, E, topk, sf, pre,
-               scale, L.ptr(top), L.ptr(grad), L.ptr(out), L.stream(logits.device))
+        out = router_topk_bwd(logits, top, grad_probs, *ctx.cfg)
         return out, None, None, None, None, None, None, None, None
+
+
+def router_topk_bwd(logits, top, grad_probs, topk, sf, pre, scale):
+    """d logits of the top-k routing (``tt_router_topk_bwd``), logits dtype."""
+    T, E = logits.shape
+    grad = grad_probs.to(logits.dtype).contiguous()
+    out = torch.empty_like(logits)
+    L.call("tt_router_topk_bwd", L.ptr(logits), L.dtype_code(logits.dtype), T, E, topk, sf, pre,
+           scale, L.ptr(top), L.ptr(grad), L.ptr(out), L.stream(logits.device))
+    return out
+
+
+class RouterGateTopK(torch.autograd.Function):
+    """Gating linear and top-k routing in one kernel (``tt_router_gate_fwd``):
+    ``(probs, routing_map, top_indices, logits)`` with ``logits = x W^T`` in
+    the router dtype. Backward: the routing gradient (``tt_router_topk_bwd``)
+    plus the gradient reaching the logits directly, then the gating linear's
+    backward as ``RouterGatingLinearFunction`` forms it (``router.py:44-58``)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, router_dtype, topk, score_function, pre_softmax, num_groups,
+                group_topk, scaling_factor, expert_bias, fixed_indices):
+        x2 = x.reshape(-1, x.shape[-1]).contiguous()
+        w = weight.contiguous()
+        T, H = x2.shape
+        E = w.shape[0]
+        dev = x2.device
+        logits = torch.empty((T, E), dtype=router_dtype, device=dev)
+        probs = torch.empty_like(logits)
+        rmap = torch.empty((T, E), dtype=torch.bool, device=dev)
+        top = torch.empty((T, topk), dtype=torch.int64, device=dev)
+        bias = None if expert_bias is None else expert_bias.to(device=dev, dtype=torch.float32).contiguous()
+        fixed = None if fixed_indices is None else fixed_indices.to(device=dev, dtype=torch.int64).contiguous()
+        sf = L.TT_SCORE[score_function]
+        cfg = (topk, sf, int(bool(pre_softmax)), float(scaling_factor or 0.0))
+        L.call("tt_router_gate_fwd", L.ptr(x2), L.ptr(w), L.dtype_code(x2.dtype), T, H, E,
+               L.dtype_code(router_dtype), topk, sf, cfg[2], L.ptr(bias), int(num_groups or 0),
+               int(group_topk or 0), cfg[3], L.ptr(fixed), L.ptr(logits), L.ptr(probs),
+               L.ptr(rmap), L.ptr(top), L.stream(dev))
+        ctx.save_for_backward(x2, w, logits, top)
+        ctx.cfg = cfg
+        ctx.x_shape = x.shape
+        ctx.mark_non_differentiable(rmap, top)
+        ctx.set_materialize_grads(False)
+        return probs, rmap, top, logits
+
+    @staticmethod
+    def backward(ctx, g_probs, _g_map, _g_top, g_logits):
+        none = (None,) * 9
+        x2, w, logits, top = ctx.saved_tensors
+        g = None
+        if g_probs is not None:
+            g = router_topk_bwd(logits, top, g_probs, *ctx.cfg)
+        if g_logits is not None:
+            g_logits = g_logits.reshape(logits.shape).to(logits.dtype)
+            g = g_logits if g is None else g + g_logits
+        if g is None:
+            return None, None, *none
+        rdt = logits.dtype
+        gx = gw = None
+        if ctx.needs_input_grad[0]:
+            gx = g.mm(w.to(rdt)).view(ctx.x_shape).to(x2.dtype)
+        if ctx.needs_input_grad[1]:
+            gw = g.t().mm(x2.to(rdt)).to(w.dtype)
+        return gx, gw, *none
 
 
 class RouterLossStats(torch.autograd.Function):

@@ -13,7 +13,7 @@ from __future__ import annotations
 from ...dispatch import OpImpl, OpImplKind, register_op
 from ...runtime import TurboDevice
 from . import PRIORITY
-from ._functions import RouterLossStats, TopKRouting, require_cuda
+from ._functions import RouterGateTopK, RouterLossStats, TopKRouting, require_cuda
 from .available import hip_available
 
 
@@ -64,3 +64,33 @@ class HipRouterLossStats(OpImpl):
             raise ValueError(f"topk must be in [1, {logits.shape[1]}], got {topk}")
         return RouterLossStats.apply(logits, int(topk), score_function, padding_mask, bool(aux),
                                      bool(z))
+
+
+@register_op(op_name="router_gate_topk", impl_name="hip_router_gate_topk",
+             kind=OpImplKind.CUSTOM, priority=PRIORITY, devices=(TurboDevice.CUDA,))
+class HipRouterGateTopK(OpImpl):
+    """``(probs, routing_map, top_indices, logits)`` of ``TopKRouter.gating``
+    (``router.py:25-58,84-101``) followed by ``topk_softmax_with_capacity``
+    (``utils.py:127-230``), in one kernel: x and the router weight in bf16 or
+    f16 (the same dtype), logits in that dtype or fp32, E a multiple of 32 up
+    to 256, hidden a multiple of 64 (``TopKRouter`` checks this before it
+    asks)."""
+
+    def available(self) -> bool:
+        return hip_available()
+
+    def __call__(self, x, weight, router_dtype, topk, use_pre_softmax=False, num_groups=None,
+                 group_topk=None, scaling_factor=None, score_function="softmax",
+                 expert_bias=None, use_hash_routing=False, hash_table=None, input_ids=None):
+        require_cuda(x, weight)
+        if score_function not in ("softmax", "sigmoid", "sqrtsoftplus"):
+            raise ValueError(f"Invalid score_function: {score_function}")
+        fixed = None
+        if use_hash_routing:
+            if hash_table is None or input_ids is None:
+                raise ValueError("Hash routing requires hash_table and input_ids.")
+            fixed = hash_table.to(x.device)[input_ids.reshape(-1).to(x.device)]
+        bias = expert_bias if score_function != "softmax" or use_pre_softmax else None
+        return RouterGateTopK.apply(x, weight, router_dtype, int(topk), score_function,
+                                    bool(use_pre_softmax), num_groups, group_topk,
+                                    scaling_factor, bias, fixed)
