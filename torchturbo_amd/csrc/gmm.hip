@@ -689,8 +689,11 @@ __device__ __forceinline__ uint32_t fragk64(int r0, int s, int lane) {
 // 16-byte chunk c in slot c ^ ((r >> 1) & 7)), stored as 128-byte row segments with
 // buffer stores. The store resource ends at the expert's last row, so
 // stores to rows past it are dropped by the hardware; columns past the
-// output width are given an offset past the resource.
-template <int ET>
+// output width are given an offset past the resource. AUX is the stores'
+// cache policy: 2 (streaming) for weight gradients, which nothing in the
+// step reads back (5 % faster on DeepSeek-V3's write-bound weight
+// gradients); 0 for activations, which the next kernel reads.
+template <int ET, int AUX>
 __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], const TileDesc& t,
                                                     int64_t ri, int64_t cj, lds_char* region) {
   // Lane index computed here (volatile, so neither it nor what derives from
@@ -740,7 +743,7 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
         const uint4 v = read_k(region, (uint32_t)(r * 128 + ((ch ^ ((r >> 1) & 7)) << 4)));
         const uint32_t off = col_ok ? (uint32_t)(32 * mi + r) * row_bytes + (uint32_t)col * 2u
                                     : DM_OOB;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (int)off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (int)off, 0, AUX);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1126,7 +1129,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     step(nkt_c - 1, g, std::true_type{});
     ++g;
     __builtin_amdgcn_sched_barrier(0);
-    store_wave_tile_p64<ET>(acc, tc, tc.i0 + wm * WT, tc.j0 + wn * WT, epi);
+    store_wave_tile_p64<ET, WG ? 2 : 0>(acc, tc, tc.i0 + wm * WT, tc.j0 + wn * WT, epi);
     if (!has_next) break;
     tc = tn;
     nkt_c = nkt_n;
@@ -1788,7 +1791,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_q8_kernel(const char* __restrict__ 
     step(nkt - 1, g, std::true_type{});
     ++g;
     __builtin_amdgcn_sched_barrier(0);
-    store_wave_tile_p64<TT_BF16>(acc, tc, tc.i0, tc.j0 + 128 * wave, epi);
+    store_wave_tile_p64<TT_BF16, 0>(acc, tc, tc.i0, tc.j0 + 128 * wave, epi);
     if (++n == ntiles) break;
     tc = tn;
     ra_cur = ra_nxt;
