@@ -11,6 +11,10 @@ ffn 768, bf16, Zipf-skewed fp32 router logits).
 Prints one JSON line with the throughput, the grouped-GEMM roofline (HIP
 events around every grouped-GEMM launch on the compute stream) and the CPU
 oracle timed on a bounded sample of the same workload.
+
+``--part router`` times the router front end instead: ``TopKRouter`` forward
+and backward on the workload's tokens (gating linear fused with the top-k,
+aux-loss and z-loss sums, 16-bit router weight, fp32 router dtype).
 """
 
 from __future__ import annotations
@@ -31,6 +35,8 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 HBM_PEAK_GBS = 8000.0
 GEMM_ENTRIES = ("tt_gmm_fwd", "tt_gmm_dgrad", "tt_gmm_wgrad", "tt_gmm_fp8_fwd", "tt_gmm_fp8_dgrad")
 PERMUTE_ENTRIES = ("tt_permute_scatter", "tt_unpermute_gather")
+ROUTER_ENTRIES = ("tt_router_gate_fwd", "tt_router_topk_fwd", "tt_router_topk_bwd",
+                  "tt_router_loss_fwd", "tt_router_loss_bwd")
 
 
 def parse():
@@ -39,6 +45,8 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="qwen3_30b_a3b")
+    p.add_argument("--part", choices=("layer", "router"), default="layer",
+                   help="layer: the MoE layer step (default); router: the router front end only")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -160,6 +168,77 @@ def gpu_run(w, steps, warmup):
     return (t1 - t0) * 1e3 / steps, kernels
 
 
+def router_run(w, steps, warmup):
+    """TopKRouter forward + backward (router.py:358-380) at the workload's size."""
+    from torchturbo_amd import _lib as L
+    from torchturbo_amd import configs as C
+    from torchturbo_amd.dispatch import OpPolicy, get_or_create_ops
+    from torchturbo_amd.moe import MoEConfig, TopKRouter
+    from torchturbo_amd.runtime import CudaRuntime
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    get_or_create_ops(device_runtime=CudaRuntime(), default_policy=OpPolicy.CUSTOM)
+    cfg = MoEConfig(
+        hidden_size=w.hidden, num_moe_experts=w.experts, moe_router_topk=w.topk,
+        moe_router_pre_softmax=w.pre_softmax, moe_router_score_function=w.score_function,
+        moe_router_num_groups=w.num_groups, moe_router_group_topk=w.group_topk,
+        moe_router_topk_scaling_factor=w.scaling_factor, params_dtype=w.dtype,
+        moe_router_enable_expert_bias=w.expert_bias, moe_router_dtype="fp32",
+        moe_aux_loss_coeff=1e-3, moe_z_loss_coeff=1e-3, perform_initialization=False,
+    )
+    router = TopKRouter(cfg).to(dev)
+    with torch.no_grad():
+        router.weight.normal_(0.0, w.hidden ** -0.5)
+    hidden = C.make_hidden(w, device=dev).requires_grad_()
+    g = torch.Generator(device=dev).manual_seed(w.seed + 3)
+    gp = torch.randn(w.tokens, w.experts, device=dev, generator=g)
+
+    def step():
+        router.weight.grad = None
+        hidden.grad = None
+        probs, _, _, _ = router(hidden)
+        (probs * gp).sum().backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = L.KernelTimer(ROUTER_ENTRIES)
+    L.set_timer(timer)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L.set_timer(None)
+    return (t1 - t0) * 1e3 / steps, timer.elapsed_ms(), router._can_fuse_gate(hidden)
+
+
+def router_line(w, args):
+    ms, kernels, fused = router_run(w, args.steps, args.warmup)
+    T, H, E = w.tokens, w.hidden, w.experts
+    avg = {n: round(v[1] / v[0] * 1e3, 1) for n, v in kernels.items() if v[0]}
+    gate_us = avg.get("tt_router_gate_fwd")
+    gate = None
+    if gate_us:
+        flops = 2.0 * T * H * E
+        nbytes = T * H * 2 + -(-T // 64) * E * H * 2 + T * E * 9 + T * w.topk * 8
+        gate = {"bound": "latency", "kernel": "tt_router_gate_fwd", "avg_launch_us": gate_us,
+                "achieved_tflops": round(flops / gate_us / 1e6, 1),
+                "achieved_gbs": round(nbytes / gate_us / 1e3, 1)}
+    return {
+        "metric": "router front end fwd+bwd tokens/sec (gating linear + top-k + aux/z-loss sums)",
+        "value": round(T / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "vs_baseline": None, "data": "synthetic",
+        "dtype": "bf16 inputs and router weight, fp32 logits",
+        "config": {"workload": w.name, "tokens": T, "hidden": H, "experts": E, "topk": w.topk,
+                   "router": w.score_function, "router_dtype": "fp32", "fused_gate": fused,
+                   "aux_loss_coeff": 1e-3, "z_loss_coeff": 1e-3},
+        "kernels_avg_us": avg, "gate": gate,
+    }
+
+
 def cpu_baseline(w, budget_s):
     """The CPU oracle (the reference's native composition) on a token sample."""
     from dataclasses import replace
@@ -226,6 +305,9 @@ def main():
     from torchturbo_amd import configs as C
 
     w = C.resolve(C.WORKLOADS[args.workload])
+    if args.part == "router":
+        print(json.dumps(router_line(w, args)), flush=True)
+        return
     ms, kernels = gpu_run(w, args.steps, args.warmup)
     tokens_per_s = w.tokens / (ms / 1e3)
 
