@@ -237,3 +237,52 @@ def test_fp8_experts_loaded_from_safetensors_on_gpu(process_ops, tmp_path):
     w2g = ref.weight2.grad.view(E, Fd, H).transpose(1, 2)
     assert_bf16_close(mod.master1.grad.cpu(), w1g, what="fp8 ckpt dw1")
     assert_bf16_close(mod.master2.grad.cpu(), w2g, what="fp8 ckpt dw2")
+
+
+def test_full_layer_forward_with_fused_router_matches_cpu(process_ops, monkeypatch):
+    """MoELayer.forward (moe_layer.py:149-183) end to end: the router's gating
+    linear fused with the top-k, aux-loss and z-loss sums, experts, combine;
+    GPU against the same layer on the CPU oracle. Seed 12: every token's 4th
+    and 5th logits differ by >= 2.3e-3, far above the difference between the
+    CPU and GPU fp32 sums of the exact bf16 products."""
+    from torchturbo_amd.moe.router import MoEAuxLossAutoScaler
+    from torchturbo_amd.runtime import CpuRuntime
+
+    monkeypatch.setattr(MoEAuxLossAutoScaler, "loss_scale", 1.0)
+    g = torch.Generator().manual_seed(12)
+    T, H, E, k, Fd = 256, 256, 64, 4, 128
+    x = torch.randn(T, H, generator=g).bfloat16()
+    wr = (torch.randn(E, H, generator=g) * 0.08).bfloat16()
+    w1 = (torch.randn(E * H, 2 * Fd, generator=g) * 0.05).bfloat16()
+    w2 = (torch.randn(E * Fd, H, generator=g) * 0.05).bfloat16()
+    grad = torch.randn(T, H, generator=g).bfloat16()
+    cfg = MoEConfig(hidden_size=H, num_moe_experts=E, moe_ffn_hidden_size=Fd,
+                    gated_linear_unit=True, activation_func=F.silu, moe_router_topk=k,
+                    moe_router_dtype="fp32", moe_aux_loss_coeff=1e-2, moe_z_loss_coeff=1e-3,
+                    params_dtype=torch.bfloat16, perform_initialization=False)
+
+    def run(runtime, policy, oracle, dev):
+        process_ops(runtime, policy, oracle=oracle)
+        layer = MoELayer(cfg, None, submodules=MoESubmodules(experts=ModuleSpec(module=GroupedMLP)))
+        layer = layer.to(dev)
+        with torch.no_grad():
+            layer.router.weight.copy_(wr)
+            layer.experts.weight1.copy_(w1)
+            layer.experts.weight2.copy_(w2)
+        assert layer.router._can_fuse_gate(x.to(dev))
+        xi = x.detach().clone().to(dev).requires_grad_()
+        out, logits = layer(xi)
+        (out.float() * grad.to(dev).float()).sum().backward()
+        m = layer.router.pop_metrics()
+        return (out.detach().cpu(), logits.detach().cpu(), xi.grad.cpu(),
+                layer.router.weight.grad.cpu(), layer.experts.weight1.grad.cpu(),
+                layer.experts.weight2.grad.cpu(), {n: v.cpu() for n, v in m.items()})
+
+    ref = run(CpuRuntime(), OpPolicy.NATIVE, True, "cpu")
+    got = run(CudaRuntime(), OpPolicy.CUSTOM, False, DEV)
+    mx, _ = rel_errors(got[1], ref[1])
+    assert mx <= 1e-5, ("logits", mx)
+    for name, a, b in zip(("out", "logits", "dx", "d_router", "d_w1", "d_w2"), got[:6], ref[:6]):
+        assert_bf16_close(a, b, what=name)
+    for key in ("aux_loss", "z_loss"):
+        torch.testing.assert_close(got[6][key], ref[6][key], rtol=1e-4, atol=0)
