@@ -138,7 +138,7 @@ __device__ __forceinline__ float load_w(const void* p, int64_t i) {
 constexpr int kNoProbs = -1;
 
 template <class TT, int XD, int PD, int V, int KMAX>
-__global__ __launch_bounds__(256) void unpermute_small_kernel(
+__global__ __launch_bounds__(1024) void unpermute_small_kernel(
     const typename TT::storage* __restrict__ packed, int64_t H, int K,
     const int32_t* __restrict__ rows, const int64_t* __restrict__ experts,
     const void* __restrict__ probs, int E, typename TT::storage* __restrict__ out, int64_t M) {
@@ -220,7 +220,10 @@ __global__ __launch_bounds__(256) void unpermute_small_kernel(
     St y[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) y[i] = TT::from_f32(rnd_dt<PR>(acc[i]));
-    __builtin_memcpy(out + t * H + v * V, y, sizeof(y));
+    // Streaming store: measured in the layer step, the token rows written
+    // this way leave the caches to the kernels that follow (Qwen unpermute
+    // 69 -> 72 % of HBM bandwidth, and the step faster).
+    store_stream<sizeof(y)>(out + t * H + v * V, y);
   }
 }
 
@@ -399,7 +402,12 @@ int launch_unpermute(const void* packed, int64_t T, int64_t H, int K, const int3
   St* o = static_cast<St*>(out);
   if (al % 16 == 0 && K <= 8) {
     constexpr int V = 16 / sizeof(St);
-    const dim3 grid((unsigned)T), blk(block_for(H / V));
+    // One thread per 16-byte column slice of the row, so that every thread
+    // issues all k row loads at once (H 4096: 512 threads).
+    const int64_t nvb = H / V;
+    const unsigned nthr =
+        nvb <= 256 ? block_for(nvb) : (unsigned)(nvb <= 1024 ? ((nvb + 63) / 64) * 64 : 1024);
+    const dim3 grid((unsigned)T), blk(nthr);
     if (probs == nullptr) {
       if (K <= 2)
         hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
