@@ -367,7 +367,10 @@ def test_route_index_bit_exact(T, E, k, skew):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("T,H,E,k", [(300, 256, 8, 2), (517, 136, 64, 6), (64, 2048, 128, 8)])
+# wide rows: one thread per 16-byte vector up to 1024 (H 4096: 512 threads; H 5000:
+# 625 vectors, idle threads; H 9216: more vectors than threads)
+@pytest.mark.parametrize("T,H,E,k", [(300, 256, 8, 2), (517, 136, 64, 6), (64, 2048, 128, 8),
+                                     (40, 4096, 8, 2), (33, 5000, 8, 3), (24, 9216, 16, 8)])
 def test_permutation_and_unpermutation_bit_exact(hip_ops, dtype, T, H, E, k):
     g = torch.Generator().manual_seed(T + H)
     ids = distinct_ids(T, E, k, seed=T)
