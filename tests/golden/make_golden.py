@@ -3,6 +3,9 @@
 * ``routing_cases.json`` — tiny routing inputs with their packed-row maps
   computed by brute-force enumeration of (expert, token) pairs
   (``oracle/route_np.py::brute_force``) and their top-k ids for fp32 logits.
+* ``router_loss_cases.json`` — tiny fp32 logits with padding rows and the
+  aux-loss / z-loss sums (per-expert score sums, top-k counts, sum of squared
+  log-sum-exps) by per-row brute force in Python floats.
 * ``toy_layer.npz`` — configuration 0 of the benchmark definition (512
   tokens, hidden 256, 8 experts, top-2, ffn 512, fp32, logits N(0, 1), weights
   N(0, 0.02), seed 0): the CPU oracle layer's routing ids, per-expert counts,
@@ -48,6 +51,50 @@ def routing_cases():
         json.dump(cases, f)
 
 
+def _loss_sums_brute_force(logits, k, score_function, pad):
+    """Per-row loops in Python floats: scores by definition, the top-k set by a
+    full sort (larger first, lower id on equal scores), log-sum-exp with math."""
+    import math
+    T, E = len(logits), len(logits[0])
+    psum, cnt, z = [0.0] * E, [0] * E, 0.0
+    for t in range(T):
+        if pad[t]:
+            continue
+        row = logits[t]
+        m = max(row)
+        if score_function == "softmax":
+            ex = [math.exp(v - m) for v in row]
+            sc = [v / sum(ex) for v in ex]
+        else:
+            f = ((lambda v: 1.0 / (1.0 + math.exp(-v))) if score_function == "sigmoid"
+                 else (lambda v: math.sqrt(v if v > 20.0 else math.log1p(math.exp(v)))))
+            r = [f(v) for v in row]
+            sc = [v / (sum(r) + 1e-20) for v in r]
+        for e in range(E):
+            psum[e] += sc[e]
+        for e in sorted(range(E), key=lambda e: (-sc[e], e))[:k]:
+            cnt[e] += 1
+        z += (m + math.log(sum(math.exp(v - m) for v in row))) ** 2
+    return psum, cnt, z
+
+
+def router_loss_cases():
+    """Aux-loss / z-loss sums (models/modules/moe/moe_utils.py:15-70) of tiny fp32
+    logits with padding rows, by brute force."""
+    cases = []
+    rng = np.random.default_rng(4321)
+    for T, E, k, sf in ((6, 4, 2, "softmax"), (9, 8, 3, "sigmoid"), (7, 16, 4, "sqrtsoftplus"),
+                        (12, 32, 8, "softmax"), (5, 64, 6, "sigmoid")):
+        logits = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+        pad = (rng.random(T) < 0.25).tolist()
+        psum, cnt, z = _loss_sums_brute_force(logits.astype(np.float64).tolist(), k, sf, pad)
+        cases.append({"T": T, "E": E, "k": k, "score_function": sf, "logits": logits.tolist(),
+                      "padding_mask": pad, "prob_sum": psum, "tokens_per_expert": cnt,
+                      "z_sum": z})
+    with open(os.path.join(HERE, "router_loss_cases.json"), "w") as f:
+        json.dump(cases, f)
+
+
 def toy_layer():
     w = C.TOY
     hidden, logits = C.make_hidden(w), C.make_logits(w)
@@ -72,5 +119,6 @@ def toy_layer():
 
 if __name__ == "__main__":
     routing_cases()
+    router_loss_cases()
     toy_layer()
     print("fixtures written to", HERE)

@@ -289,6 +289,26 @@ def test_router_loss_stats_matches_oracle(hip_ops, case):
         assert_bf16_close(dev.grad.cpu(), ref.grad, what="dlogits")
 
 
+def test_router_loss_stats_match_golden_brute_force(hip_ops):
+    """tests/golden/router_loss_cases.json (per-row brute force in Python floats,
+    padding rows included) through the HIP kernels."""
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(__file__), "golden", "router_loss_cases.json")
+    with open(path) as f:
+        cases = json.load(f)
+    for c in cases:
+        logits = torch.tensor(c["logits"], dtype=torch.float32, device=DEV)
+        pad = torch.tensor(c["padding_mask"], dtype=torch.bool, device=DEV)
+        ps, cn, zs = hip_ops.router_loss_stats(logits, c["k"], c["score_function"], pad)
+        torch.testing.assert_close(ps.cpu().double(), torch.tensor(c["prob_sum"], dtype=torch.float64),
+                                   rtol=1e-5, atol=1e-6)
+        assert cn.cpu().tolist() == c["tokens_per_expert"]
+        torch.testing.assert_close(zs.cpu().double(), torch.tensor(c["z_sum"], dtype=torch.float64),
+                                   rtol=1e-5, atol=1e-6)
+
+
 def test_router_loss_stats_is_reproducible(hip_ops):
     g = torch.Generator().manual_seed(1)
     logits = torch.randn(50000, 128, generator=g).to(DEV)

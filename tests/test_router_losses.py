@@ -215,3 +215,23 @@ def test_fused_gate_path_equals_reference_composition(cpu_ops, rdt):
             assert_bf16_close(u, v)
         else:
             torch.testing.assert_close(u, v)
+
+
+def test_oracle_loss_stats_match_golden_brute_force():
+    """tests/golden/router_loss_cases.json: per-row brute force in Python floats
+    (make_golden.py), padding rows included."""
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(__file__), "golden", "router_loss_cases.json")
+    with open(path) as f:
+        cases = json.load(f)
+    for c in cases:
+        logits = torch.tensor(c["logits"], dtype=torch.float32)
+        pad = torch.tensor(c["padding_mask"], dtype=torch.bool)
+        ps, cn, zs = router_loss_stats(logits, c["k"], c["score_function"], pad)
+        torch.testing.assert_close(ps.double(), torch.tensor(c["prob_sum"], dtype=torch.float64),
+                                   rtol=1e-5, atol=1e-6)
+        assert cn.tolist() == c["tokens_per_expert"]
+        torch.testing.assert_close(zs.double(), torch.tensor(c["z_sum"], dtype=torch.float64),
+                                   rtol=1e-5, atol=1e-6)
