@@ -141,6 +141,8 @@ GATE_CASES = [
     (65, 128, 160, 6, "softmax", True, None, None, 1.5, True, torch.float16, torch.float32),
     (129, 192, 64, 4, "softmax", False, None, None, None, False, torch.bfloat16, torch.bfloat16),
     (0, 256, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16, torch.float32),
+    # 64-token blocks (the grid covers the device); the cases above use 32-token blocks
+    (16448, 128, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16, torch.float32),
 ]
 
 

@@ -927,7 +927,6 @@ typedef __attribute__((ext_vector_type(4))) unsigned gu32x4;
 typedef __attribute__((address_space(3))) char glds_char;
 typedef __attribute__((address_space(3))) gu32x4 glds_u32x4;
 
-constexpr int kGateTokens = 64;
 constexpr int kGateRow = 128;  // bytes of one row of a 64-deep chunk
 
 #define RG_WAIT_VMCNT(n) \
@@ -971,40 +970,43 @@ __device__ __forceinline__ gf32x16 rg_mma<TT_F16>(const uint4& a, const uint4& b
                                                  __builtin_bit_cast(gf16x8, b), c, 0, 0, 0);
 }
 
-template <int P>
+// N 32-expert tiles (E = 32 N), TOK tokens per block (64, or 32 when 64-token
+// blocks would leave compute units idle).
+template <int N, int TOK>
 struct GateShape {
-  static constexpr int E = 32 * P - 64;                    // experts
-  static constexpr int NT = E / 32;                         // 32-expert tiles
-  static constexpr int WAVES = 16;                          // waves per block
-  static constexpr int TPW = (2 * NT + WAVES - 1) / WAVES;  // 32x32 output tiles per wave
-  static constexpr int NI = 4 * P;                          // DMA loads per chunk (8 rows each)
-  static constexpr int PW = (NI + WAVES - 1) / WAVES;       // ... per wave (the rest: dummy)
-  static constexpr int SB = (kGateTokens + E) * kGateRow;   // stage bytes
+  static constexpr int E = 32 * N;                              // experts
+  static constexpr int NT = N;                                  // 32-expert tiles
+  static constexpr int MT = TOK / 32;                           // 32-token tiles
+  static constexpr int WAVES = 16;                              // waves per block
+  static constexpr int TPW = (MT * NT + WAVES - 1) / WAVES;     // 32x32 output tiles per wave
+  static constexpr int NI = (TOK + E) / 8;                      // DMA loads per chunk (8 rows)
+  static constexpr int PW = (NI + WAVES - 1) / WAVES;           // ... per wave (rest: dummy)
+  static constexpr int SB = (TOK + E) * kGateRow;               // stage bytes
   static constexpr int NS = 4 * SB + 1024 <= 128 * 1024 ? 4 : 3;  // stages in the ring
-  static constexpr int LS = E + 4;                          // logits tile row stride (floats)
+  static constexpr int LS = E + 4;                              // logits tile row stride (floats)
   static constexpr int EPL = E <= 64 ? 1 : (E <= 128 ? 2 : 4);
-  static constexpr int RING = NS * SB + 1024;               // + a dummy DMA target
-  static constexpr int LDS = RING > kGateTokens * LS * 4 ? RING : kGateTokens * LS * 4;
+  static constexpr int RING = NS * SB + 1024;                   // + a dummy DMA target
+  static constexpr int LDS = RING > TOK * LS * 4 ? RING : TOK * LS * 4;
 };
 
 // 16 waves: the GEMM gives each wave one or two 32x32 (token, expert) tiles;
-// the selection then routes 4 tokens per wave.
-template <int ET, int P>
+// the selection then routes TOK / 16 tokens per wave.
+template <int ET, int N, int TOK>
 __global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
     const char* __restrict__ x, const char* __restrict__ w, int64_t T, int H, int ldt, int K,
     int score_fn, int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
     const int64_t* __restrict__ fixed, void* __restrict__ logits, void* __restrict__ probs,
     uint8_t* __restrict__ rmap, int64_t* __restrict__ top_idx) {
-  typedef GateShape<P> S;
-  constexpr int E = S::E, NS = S::NS, SB = S::SB, EPL = S::EPL, PW = S::PW;
+  typedef GateShape<N, TOK> S;
+  constexpr int E = S::E, NS = S::NS, SB = S::SB, EPL = S::EPL, PW = S::PW, MT = S::MT;
   extern __shared__ __align__(16) char gsm[];
   glds_char* const lds = (glds_char*)gsm;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t t0 = (int64_t)blockIdx.x * kGateTokens;
+  const int64_t t0 = (int64_t)blockIdx.x * TOK;
   const int nch = H / 64;
-  const int64_t nrow = T - t0 < kGateTokens ? T - t0 : kGateTokens;
+  const int64_t nrow = T - t0 < TOK ? T - t0 : TOK;
   const gi32x4 rx = rg_rsrc(x + t0 * H * 2, nrow * H * 2);
   const gi32x4 rw = rg_rsrc(w, (int64_t)E * H * 2);
 
@@ -1017,10 +1019,10 @@ __global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
     for (int q = 0; q < PW; ++q) {
       const int g = wave * PW + q;
       const bool real = g < S::NI;
-      const bool isx = 8 * g < kGateTokens;
+      const bool isx = 8 * g < TOK;
       const int r = 8 * g + (lane >> 3);
       const int c = (lane & 7) ^ ((r >> 1) & 7);
-      const int orow = isx ? r : r - kGateTokens;
+      const int orow = isx ? r : r - TOK;
       const uint32_t off = (uint32_t)(((int64_t)orow * H + (int64_t)kc * 64 + c * 8) * 2);
       const bool live = real && kc < nch;
       gi32x4 rs;
@@ -1051,13 +1053,13 @@ __global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
       const int c = 2 * s + (lane >> 5);
 #pragma unroll
       for (int i = 0; i < S::TPW; ++i) {
-        const int tile = wave + S::WAVES * i;  // token tile tile & 1, expert tile tile >> 1
-        if (tile < 2 * S::NT) {
+        const int tile = wave + S::WAVES * i;  // token tile tile % MT, expert tile tile / MT
+        if (tile < MT * S::NT) {
           const uint4 a = __builtin_bit_cast(uint4, *reinterpret_cast<const glds_u32x4*>(
-                                                        st + rg_swz(32 * (tile & 1) + (lane & 31), c)));
+                                                        st + rg_swz(32 * (tile % MT) + (lane & 31), c)));
           const uint4 b = __builtin_bit_cast(
               uint4, *reinterpret_cast<const glds_u32x4*>(
-                         st + rg_swz(kGateTokens + 32 * (tile >> 1) + (lane & 31), c)));
+                         st + rg_swz(TOK + 32 * (tile / MT) + (lane & 31), c)));
           acc[i] = rg_mma<ET>(b, a, acc[i]);
         }
       }
@@ -1072,11 +1074,11 @@ __global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
 #pragma unroll
   for (int i = 0; i < S::TPW; ++i) {
     const int tile = wave + S::WAVES * i;
-    if (tile >= 2 * S::NT) continue;
-    const int row = 32 * (tile & 1) + (lane & 31);
+    if (tile >= MT * S::NT) continue;
+    const int row = 32 * (tile % MT) + (lane & 31);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int col = 32 * (tile >> 1) + 8 * q + 4 * (lane >> 5);
+      const int col = 32 * (tile / MT) + 8 * q + 4 * (lane >> 5);
       float4 v;
       v.x = round_to(acc[i][4 * q + 0], ldt);
       v.y = round_to(acc[i][4 * q + 1], ldt);
@@ -1086,11 +1088,11 @@ __global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < kGateTokens * E; idx += 64 * S::WAVES) {
+  for (int idx = tid; idx < TOK * E; idx += 64 * S::WAVES) {
     const int row = idx / E, col = idx % E;
     if (row < nrow) store_from_f32(logits, ldt, (t0 + row) * E + col, L[row * S::LS + col]);
   }
-  constexpr int RPW = kGateTokens / S::WAVES;  // tokens routed per wave
+  constexpr int RPW = TOK / S::WAVES;  // tokens routed per wave
   for (int rr = 0; rr < RPW; ++rr) {
     const int row = wave * RPW + rr;
     if (row >= nrow) break;  // wave-uniform; no block synchronisation follows
@@ -1107,16 +1109,16 @@ __global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
   }
 }
 
-template <int ET, int P>
-int launch_gate(const void* x, const void* w, int64_t T, int H, int ldt, int K, int sf, int pre,
-                const float* bias, int G, int GK, float scale, const int64_t* fixed, void* logits,
-                void* probs, uint8_t* rmap, int64_t* top, hipStream_t s) {
-  typedef GateShape<P> S;
+template <int ET, int N, int TOK>
+int launch_gate_t(const void* x, const void* w, int64_t T, int H, int ldt, int K, int sf, int pre,
+                  const float* bias, int G, int GK, float scale, const int64_t* fixed,
+                  void* logits, void* probs, uint8_t* rmap, int64_t* top, hipStream_t s) {
+  typedef GateShape<N, TOK> S;
   static_assert(S::LDS <= 160 * 1024, "gate tile exceeds LDS");
   static bool allowed = false;  // the attribute belongs to the kernel, for every device
   if (!allowed) {
     const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&router_gate_fwd_kernel<ET, P>),
+        reinterpret_cast<const void*>(&router_gate_fwd_kernel<ET, N, TOK>),
         hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS);
     if (e != hipSuccess) {
       (void)hipGetLastError();
@@ -1126,11 +1128,37 @@ int launch_gate(const void* x, const void* w, int64_t T, int H, int ldt, int K, 
     }
     allowed = true;
   }
-  const dim3 grid((unsigned)((T + kGateTokens - 1) / kGateTokens));
-  hipLaunchKernelGGL((router_gate_fwd_kernel<ET, P>), grid, dim3(64 * S::WAVES), S::LDS, s,
+  const dim3 grid((unsigned)((T + TOK - 1) / TOK));
+  hipLaunchKernelGGL((router_gate_fwd_kernel<ET, N, TOK>), grid, dim3(64 * S::WAVES), S::LDS, s,
                      static_cast<const char*>(x), static_cast<const char*>(w), T, H, ldt, K, sf,
                      pre, bias, G, GK, scale, fixed, logits, probs, rmap, top);
   return tt_check_launch("router_gate_fwd");
+}
+
+// Compute units of the current device, cached per device.
+int gate_cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// 64 tokens per block, or 32 when 64-token blocks would not cover the device.
+template <int ET, int N>
+int launch_gate(const void* x, const void* w, int64_t T, int H, int ldt, int K, int sf, int pre,
+                const float* bias, int G, int GK, float scale, const int64_t* fixed, void* logits,
+                void* probs, uint8_t* rmap, int64_t* top, hipStream_t s) {
+  if ((T + 63) / 64 < gate_cu_count())
+    return launch_gate_t<ET, N, 32>(x, w, T, H, ldt, K, sf, pre, bias, G, GK, scale, fixed,
+                                    logits, probs, rmap, top, s);
+  return launch_gate_t<ET, N, 64>(x, w, T, H, ldt, K, sf, pre, bias, G, GK, scale, fixed, logits,
+                                  probs, rmap, top, s);
 }
 
 int epl_for(int E) {
@@ -1388,46 +1416,23 @@ extern "C" int tt_router_gate_fwd(const void* x, const void* weight, int in_dtyp
   if (num_tokens == 0) return TT_OK;
   const int gk = fixed_indices ? 0 : group_topk;
   const int H = (int)hidden;
-  const int P = (num_experts + 64) / 32;
-#define TT_GATE(ET)                                                                          \
-  switch (P) {                                                                               \
-    case 3: return launch_gate<ET, 3>(x, weight, num_tokens, H, logits_dtype, topk,          \
-                                      score_function, pre_softmax, expert_bias, num_groups,  \
-                                      gk, scaling_factor, fixed_indices, logits, probs,      \
-                                      routing_map, top_indices, S(stream));                  \
-    case 4: return launch_gate<ET, 4>(x, weight, num_tokens, H, logits_dtype, topk,          \
-                                      score_function, pre_softmax, expert_bias, num_groups,  \
-                                      gk, scaling_factor, fixed_indices, logits, probs,      \
-                                      routing_map, top_indices, S(stream));                  \
-    case 5: return launch_gate<ET, 5>(x, weight, num_tokens, H, logits_dtype, topk,          \
-                                      score_function, pre_softmax, expert_bias, num_groups,  \
-                                      gk, scaling_factor, fixed_indices, logits, probs,      \
-                                      routing_map, top_indices, S(stream));                  \
-    case 6: return launch_gate<ET, 6>(x, weight, num_tokens, H, logits_dtype, topk,          \
-                                      score_function, pre_softmax, expert_bias, num_groups,  \
-                                      gk, scaling_factor, fixed_indices, logits, probs,      \
-                                      routing_map, top_indices, S(stream));                  \
-    case 7: return launch_gate<ET, 7>(x, weight, num_tokens, H, logits_dtype, topk,          \
-                                      score_function, pre_softmax, expert_bias, num_groups,  \
-                                      gk, scaling_factor, fixed_indices, logits, probs,      \
-                                      routing_map, top_indices, S(stream));                  \
-    case 8: return launch_gate<ET, 8>(x, weight, num_tokens, H, logits_dtype, topk,          \
-                                      score_function, pre_softmax, expert_bias, num_groups,  \
-                                      gk, scaling_factor, fixed_indices, logits, probs,      \
-                                      routing_map, top_indices, S(stream));                  \
-    case 9: return launch_gate<ET, 9>(x, weight, num_tokens, H, logits_dtype, topk,          \
-                                      score_function, pre_softmax, expert_bias, num_groups,  \
-                                      gk, scaling_factor, fixed_indices, logits, probs,      \
-                                      routing_map, top_indices, S(stream));                  \
-    default: return launch_gate<ET, 10>(x, weight, num_tokens, H, logits_dtype, topk,        \
-                                        score_function, pre_softmax, expert_bias, num_groups, \
-                                        gk, scaling_factor, fixed_indices, logits, probs,     \
-                                        routing_map, top_indices, S(stream));                 \
+  const int NE = num_experts / 32;
+#define TT_GATE_N(ET, NN)                                                                       \
+  case NN:                                                                                     \
+    return launch_gate<ET, NN>(x, weight, num_tokens, H, logits_dtype, topk, score_function,   \
+                               pre_softmax, expert_bias, num_groups, gk, scaling_factor,       \
+                               fixed_indices, logits, probs, routing_map, top_indices,         \
+                               S(stream));
+#define TT_GATE(ET)                                                                            \
+  switch (NE) {                                                                                \
+    TT_GATE_N(ET, 1) TT_GATE_N(ET, 2) TT_GATE_N(ET, 3) TT_GATE_N(ET, 4)                        \
+    TT_GATE_N(ET, 5) TT_GATE_N(ET, 6) TT_GATE_N(ET, 7) default: TT_GATE_N(ET, 8)               \
   }
   if (in_dtype == TT_BF16) {
     TT_GATE(TT_BF16)
   } else {
     TT_GATE(TT_F16)
   }
+#undef TT_GATE_N
 #undef TT_GATE
 }
