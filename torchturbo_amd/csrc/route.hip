@@ -423,7 +423,7 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kLossWaves = 4;
 constexpr int kLossMaxBlocks = 512;
-constexpr int kLossTokensPerWave = 8;
+constexpr int kLossTokensPerWave = 2;  // at least; large batches hit the block cap
 
 int loss_blocks(int64_t T) {
   const int64_t per = (int64_t)kLossWaves * kLossTokensPerWave;
