@@ -140,6 +140,7 @@ GATE_CASES = [
     (100, 64, 32, 2, "sqrtsoftplus", False, None, None, None, False, torch.bfloat16, torch.float32),
     (65, 128, 160, 6, "softmax", True, None, None, 1.5, True, torch.float16, torch.float32),
     (129, 192, 64, 4, "softmax", False, None, None, None, False, torch.bfloat16, torch.bfloat16),
+    (200, 256, 96, 4, "sigmoid", False, None, None, None, False, torch.float16, torch.float16),
     (0, 256, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16, torch.float32),
     # 64-token blocks (the grid covers the device); the cases above use 32-token blocks
     (16448, 128, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16, torch.float32),
@@ -244,6 +245,7 @@ LOSS_CASES = [
     (300, 160, 6, "sqrtsoftplus", torch.float32, True),
     (20000, 64, 4, "softmax", torch.float32, True),  # several tokens per wave
     (1024, 128, 8, "softmax", torch.bfloat16, False),
+    (700, 64, 4, "sigmoid", torch.float16, True),
     (5, 1024, 1, "sigmoid", torch.float32, False),
     (0, 16, 2, "softmax", torch.float32, False),
 ]
