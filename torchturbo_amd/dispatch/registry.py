@@ -1,9 +1,17 @@
-"""Process-wide operator registry and the ``register_op`` decorator.
+"""Which implementations exist for each op, and the order ``auto`` tries them.
 
-Ranking follows ``src/torchturbo/ops/registry.py:35-53``: priority first, then
-device-specific over device-agnostic, then custom over native, descending.
-Re-registering an ``impl_name`` replaces it in place; the same ``impl_name``
-under a different op is an error (``registry.py:14-31``).
+Behaviour callers rely on (the reference's ``src/torchturbo/ops/registry.py:35-85``):
+
+* an implementation is known by its ``impl_name``. Registering a name again for
+  the same op replaces the earlier spec where it stood; the same name under a
+  different op is a ``ValueError``;
+* ``list()`` ranks candidates by priority, then device-specific (non-empty
+  ``devices``) before device-agnostic, then custom before native, each
+  descending; equal candidates keep their registration order.
+
+The table is a dict keyed by ``impl_name``: a dict remembers insertion order and
+assigning to an existing key keeps that key's position, which is exactly the
+replace-in-place rule, so no separate ordered list is kept.
 """
 
 from __future__ import annotations
@@ -14,40 +22,36 @@ from ..runtime import TurboDevice
 from .base import OpImpl, OpImplKind, OpSpec
 
 
+def _rank(spec: OpSpec) -> tuple[int, int, int]:
+    """Sort key of ``list()`` (larger ranks first)."""
+    return (spec.priority, 1 if spec.devices else 0, 1 if spec.kind == OpImplKind.CUSTOM else 0)
+
+
 class OpRegistry:
     def __init__(self) -> None:
-        self._specs: list[OpSpec] = []
-        self._by_impl: dict[str, OpSpec] = {}
+        self._table: dict[str, OpSpec] = {}
 
     def register(self, spec: OpSpec) -> OpSpec:
-        existing = self._by_impl.get(spec.impl_name)
-        if existing is not None and existing.op_name != spec.op_name:
+        prior = self._table.get(spec.impl_name)
+        if prior is not None and prior.op_name != spec.op_name:
             raise ValueError(
-                f"OpSpec.impl_name {spec.impl_name!r} is already registered for "
-                f"op {existing.op_name!r}."
+                f"impl_name {spec.impl_name!r} cannot serve op {spec.op_name!r}: it is "
+                f"already registered for op {prior.op_name!r}."
             )
-        for slot, current in enumerate(self._specs):
-            if current.impl_name == spec.impl_name:
-                self._specs[slot] = spec
-                break
-        else:
-            self._specs.append(spec)
-        self._by_impl[spec.impl_name] = spec
+        self._table[spec.impl_name] = spec
         return spec
 
     def list(self, spec_filter: Callable[[OpSpec], bool] | None = None) -> list[OpSpec]:
-        specs = [s for s in self._specs if spec_filter is None or spec_filter(s)]
-        specs.sort(
-            key=lambda s: (s.priority, bool(s.devices), s.kind == OpImplKind.CUSTOM),
-            reverse=True,
-        )
-        return specs
+        """Registered specs passing ``spec_filter``, best candidate first."""
+        keep = spec_filter or (lambda _spec: True)
+        # sorted() is stable, also with reverse=True: ties stay in table order
+        return sorted((s for s in self._table.values() if keep(s)), key=_rank, reverse=True)
 
     def get_by_impl_name(self, impl_name: str) -> OpSpec:
-        spec = self._by_impl.get(impl_name)
-        if spec is None:
-            raise RuntimeError(f"No OpSpec registered for impl_name {impl_name!r}.")
-        return spec
+        try:
+            return self._table[impl_name]
+        except KeyError:
+            raise RuntimeError(f"No OpSpec registered for impl_name {impl_name!r}.") from None
 
 
 registry = OpRegistry()
@@ -61,16 +65,17 @@ def register_op(
     priority: int,
     devices: tuple[TurboDevice, ...],
 ):
-    def decorator(cls: type[OpImpl]) -> type[OpImpl]:
-        spec = OpSpec(
-            op_name=op_name, impl_name=impl_name, kind=kind,
-            priority=priority, devices=devices,
-        )
+    """Class decorator: builds the ``OpSpec`` (validated by its constructor),
+    attaches it to the ``OpImpl`` subclass as ``__op_spec__`` and registers it."""
+    spec = OpSpec(op_name=op_name, impl_name=impl_name, kind=kind, priority=priority,
+                  devices=devices)
+
+    def attach(cls: type[OpImpl]) -> type[OpImpl]:
         cls.__op_spec__ = spec
         registry.register(spec)
         return cls
 
-    return decorator
+    return attach
 
 
 __all__ = ["OpRegistry", "register_op", "registry"]
