@@ -110,17 +110,25 @@ int tt_router_loss_bwd(const void* logits, int logits_dtype, int64_t num_tokens,
  * (ops/providers/native/moe_permutation.py:36-56: masked_select of token ids,
  * masked_scatter_ of packed rows, gather by expert_indices) and the counts of
  * MoEAlltoAllTokenDispatcher.preprocess (models/modules/moe/token_dispatcher.py:125-147).
- * expert_indices [T, k] int64 (distinct per token) ->
+ * expert_indices [T, k] int64 (k distinct ids in [0, E) per token) ->
  *   row_indices [T, k] int32: packed row of (t, slot j), rows ordered by
  *     expert then token (ops/moe.py:10-46);
  *   token_of_row [T*k] int32: source token of each packed row;
  *   packed_probs [T*k] (probs dtype) = probs_dense[t, e] of each row, if both
  *     pointers are non-NULL;
  *   tokens_per_expert [E] int64.
- * Invalid ids (outside [0, E)) are not written anywhere; the call then
- * reports nothing on the host (no synchronisation), so callers validate ids.
+ * A slot whose id lies outside [0, E), or repeats an id of an earlier slot
+ * of the same token, is rejected: it gets row_indices = -1 (which the
+ * permute / unpermute kernels skip), no packed row and no count, so the
+ * counts then sum to fewer than T*k rows. The call does not synchronise the
+ * host; the number of rejected slots is written, as an int32, at byte offset
+ * tt_route_index_rejected_offset(T, E) of the workspace, for the caller to
+ * read once the stream has reached it. Only expert_indices is read: a
+ * routing map that disagrees with it is the caller's error (the reference
+ * requires the two to match, ops/dispatcher.py:559-562).
  * Workspace: tt_route_index_workspace(T, E) bytes. */
 size_t tt_route_index_workspace(int64_t num_tokens, int32_t num_experts);
+size_t tt_route_index_rejected_offset(int64_t num_tokens, int32_t num_experts);
 int tt_route_index(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
                    int32_t num_experts, const void* probs_dense, int probs_dtype,
                    int32_t* row_indices, int32_t* token_of_row, void* packed_probs,

@@ -35,6 +35,7 @@ _PROTOS: dict[str, list] = {
     "tt_router_topk_fwd": [P, c_int, I64, I32, I32, I32, I32, P, I32, I32, c_float, P, P, P, P, P],
     "tt_router_topk_bwd": [P, c_int, I64, I32, I32, I32, I32, c_float, P, P, P, P],
     "tt_route_index_workspace": [I64, I32],
+    "tt_route_index_rejected_offset": [I64, I32],
     "tt_router_gate_fwd": [P, P, c_int, I64, I64, I32, c_int, I32, I32, I32, P, I32, I32, c_float,
                            P, P, P, P, P, P],
     "tt_router_loss_workspace": [I64, I32],
@@ -57,7 +58,7 @@ _PROTOS: dict[str, list] = {
     "tt_gmm_fp8_dgrad": [P, P, P, c_int, I64, I64, I64, I32, P, P, P],
 }
 _RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_route_index_workspace": c_size_t,
-             "tt_router_loss_workspace": c_size_t}
+             "tt_route_index_rejected_offset": c_size_t, "tt_router_loss_workspace": c_size_t}
 ABI_VERSION = 1
 
 _LIB: ctypes.CDLL | None = None
@@ -152,6 +153,10 @@ def stream(device: torch.device | None = None):
 
 def route_index_workspace(num_tokens: int, num_experts: int) -> int:
     return int(load().tt_route_index_workspace(num_tokens, num_experts))
+
+
+def route_index_rejected_offset(num_tokens: int, num_experts: int) -> int:
+    return int(load().tt_route_index_rejected_offset(num_tokens, num_experts))
 
 
 def router_loss_workspace(num_tokens: int, num_experts: int) -> int:

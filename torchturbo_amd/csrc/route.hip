@@ -717,26 +717,52 @@ __global__ __launch_bounds__(256) void router_loss_bwd_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kIdxBlock = 256;  // tokens per block
 
+// Slot j of token t is accepted when its id lies in [0, E) and no earlier
+// slot of the token holds the same id; rejected slots get row -1 (skipped by
+// every later kernel) and are counted, so a caller can detect bad routing.
+__device__ __forceinline__ bool route_slot_ok(const int64_t* __restrict__ ids_t, int j,
+                                              int64_t e, int E) {
+  if (e < 0 || e >= E) return false;
+  for (int i = 0; i < j; ++i)
+    if (ids_t[i] == e) return false;
+  return true;
+}
+
+// Per-block expert histograms (bc[e * nb + block]) and per-block counts of
+// rejected slots (bad[block]); every entry is written, so nothing needs
+// clearing between calls.
 __global__ __launch_bounds__(kIdxBlock) void route_hist_kernel(
-    const int64_t* __restrict__ ids, int64_t T, int K, int E, int nb, int* __restrict__ bc) {
+    const int64_t* __restrict__ ids, int64_t T, int K, int E, int nb, int* __restrict__ bc,
+    int* __restrict__ bad) {
   extern __shared__ int hist[];
+  __shared__ int nbad;
   for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+  if (threadIdx.x == 0) nbad = 0;
   __syncthreads();
   const int64_t t = (int64_t)blockIdx.x * kIdxBlock + threadIdx.x;
   if (t < T) {
+    const int64_t* ids_t = ids + t * K;
+    int rejected = 0;
     for (int j = 0; j < K; ++j) {
-      const int64_t e = ids[t * K + j];
-      if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+      const int64_t e = ids_t[j];
+      if (route_slot_ok(ids_t, j, e, E)) atomicAdd(&hist[e], 1);
+      else ++rejected;
     }
+    if (rejected) atomicAdd(&nbad, rejected);
   }
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += blockDim.x) bc[(int64_t)e * nb + blockIdx.x] = hist[e];
+  if (threadIdx.x == 0) bad[blockIdx.x] = nbad;
 }
 
 // One wave per expert: exclusive scan of its per-block counts, in place.
+// Block 0 also adds the per-block rejected counts (fixed lane order) into
+// *bad_total.
 __global__ __launch_bounds__(64) void route_scan_kernel(int* __restrict__ bc, int nb, int E,
                                                         int* __restrict__ totals,
-                                                        int64_t* __restrict__ counts) {
+                                                        int64_t* __restrict__ counts,
+                                                        const int* __restrict__ bad,
+                                                        int* __restrict__ bad_total) {
   const int e = blockIdx.x;
   const int lane = threadIdx.x;
   int* col = bc + (int64_t)e * nb;
@@ -756,6 +782,12 @@ __global__ __launch_bounds__(64) void route_scan_kernel(int* __restrict__ bc, in
   if (lane == 0) {
     totals[e] = running;
     counts[e] = running;
+  }
+  if (e == 0) {
+    int sum = 0;
+    for (int i = lane; i < nb; i += TT_WAVE) sum += bad[i];
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, TT_WAVE);
+    if (lane == 0) *bad_total = sum;
   }
 }
 
@@ -817,6 +849,12 @@ __global__ __launch_bounds__(kIdxBlock) void route_rank_kernel(
       my[j] = (e >= 0 && e < E) ? (int)e : -1;
     }
   }
+  // A repeated id keeps its first slot only (as the histogram counted it).
+#pragma unroll
+  for (int j = 1; j < KMAX; ++j)
+#pragma unroll
+    for (int i = 0; i < j; ++i)
+      if (my[j] >= 0 && my[i] == my[j]) my[j] = -1;
 #pragma unroll
   for (int j = 0; j < KMAX; ++j)
     if (my[j] >= 0) atomicAdd(&wbase[wave * E + my[j]], 1);
@@ -1242,9 +1280,15 @@ extern "C" int tt_router_topk_bwd(const void* logits, int logits_dtype, int64_t 
   return tt_check_launch("router_bwd");
 }
 
+// Workspace: bc [nb * E] | totals [E] | bad [nb] | bad_total [1], int32.
 extern "C" size_t tt_route_index_workspace(int64_t num_tokens, int32_t num_experts) {
   const int64_t nb = (num_tokens + kIdxBlock - 1) / kIdxBlock;
-  return (size_t)(nb * num_experts + num_experts) * sizeof(int) + 256;
+  return (size_t)(nb * num_experts + num_experts + nb + 1) * sizeof(int) + 256;
+}
+
+extern "C" size_t tt_route_index_rejected_offset(int64_t num_tokens, int32_t num_experts) {
+  const int64_t nb = (num_tokens + kIdxBlock - 1) / kIdxBlock;
+  return (size_t)(nb * num_experts + num_experts + nb) * sizeof(int);
 }
 
 extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
@@ -1264,16 +1308,18 @@ extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens,
   const int nb = (int)((num_tokens + kIdxBlock - 1) / kIdxBlock);
   int* bc = static_cast<int*>(workspace);
   int* totals = bc + (int64_t)nb * num_experts;
+  int* bad = totals + num_experts;
+  int* bad_total = bad + nb;
   if (num_tokens == 0) {
     // Counts are all zero; a one-wave scan over zero blocks writes them.
     hipLaunchKernelGGL(route_scan_kernel, dim3(num_experts), dim3(64), 0, s, bc, 0, num_experts,
-                       totals, tokens_per_expert);
+                       totals, tokens_per_expert, bad, bad_total);
     return tt_check_launch("route_scan");
   }
   hipLaunchKernelGGL(route_hist_kernel, dim3(nb), dim3(kIdxBlock), num_experts * sizeof(int), s,
-                     expert_indices, num_tokens, topk, num_experts, nb, bc);
+                     expert_indices, num_tokens, topk, num_experts, nb, bc, bad);
   hipLaunchKernelGGL(route_scan_kernel, dim3(num_experts), dim3(64), 0, s, bc, nb, num_experts,
-                     totals, tokens_per_expert);
+                     totals, tokens_per_expert, bad, bad_total);
   const bool masks = num_experts <= kMaskExperts;
   const size_t lds = (size_t)5 * num_experts * sizeof(int) +
                      (masks ? (size_t)(num_experts & 1) * 4 + (size_t)4 * num_experts * 8 : 0);

@@ -21,6 +21,7 @@ from __future__ import annotations
 import torch
 
 from ... import _lib as L
+from ... import checks
 
 
 def require_cuda(*tensors: torch.Tensor | None) -> torch.device:
@@ -228,6 +229,14 @@ def route_index(expert_indices: torch.Tensor, num_experts: int, probs: torch.Ten
            L.dtype_code(probs.dtype) if probs is not None else 0, L.ptr(rows),
            L.ptr(token_of_row), L.ptr(packed_probs), L.ptr(counts), L.ptr(ws), ws_bytes,
            L.stream(dev))
+    if checks.enabled():
+        off = L.route_index_rejected_offset(T, num_experts)
+        rejected = int(ws[off:off + 4].view(torch.int32).item())
+        if rejected:
+            raise ValueError(
+                f"expert_indices must hold {K} distinct expert ids in [0, {num_experts}) per "
+                f"token: {rejected} of {T * K} slots are out of range or repeated."
+            )
     return rows, token_of_row, packed_probs, counts
 
 

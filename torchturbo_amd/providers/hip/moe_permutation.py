@@ -19,6 +19,7 @@ from dataclasses import dataclass
 import torch
 
 from ... import _lib as L
+from ... import checks
 from ...dispatch import MoEPermutation, OpImpl, OpImplKind, register_op
 from ...runtime import TurboDevice
 from . import PRIORITY
@@ -47,8 +48,31 @@ class HipMoEMaskPermutation(OpImpl):
             raise ValueError("expert_indices is required")
         if expert_indices.shape[0] != tokens.shape[0]:
             raise ValueError("expert_indices must have one row per token")
+        if routing_map.shape[0] != tokens.shape[0]:
+            raise ValueError("routing_map must have one row per token")
         packed, pprobs, rows, counts = Permute.apply(tokens, probs, expert_indices, num_experts)
+        if checks.enabled():  # after the id check inside the routing index
+            _check_map_matches_indices(routing_map, expert_indices)
         return HipMoEPermutation(packed, pprobs, rows, expert_indices, counts)
+
+
+def _check_map_matches_indices(routing_map, expert_indices):
+    """The packed order comes from expert_indices alone; the reference builds it
+    from routing_map (native/moe_permutation.py:36-51) and requires the two to
+    agree (ops/dispatcher.py:559-562). Ids outside [0, E) and repeated ids are
+    caught by the routing index itself."""
+    T, K = expert_indices.shape
+    if T == 0:
+        return
+    per_token = routing_map.bool().sum(dim=1)
+    ids = expert_indices.clamp(0, routing_map.shape[1] - 1)
+    agree = routing_map.bool().gather(1, ids).all(dim=1) & (per_token == K)
+    if not bool(agree.all()):
+        bad = int((~agree).sum())
+        raise ValueError(
+            f"routing_map and expert_indices disagree for {bad} of {T} tokens: each token's "
+            f"routing_map row must select exactly its {K} expert_indices."
+        )
 
 
 @register_op(op_name="moe_unpermutation", impl_name="hip_moe_mask_unpermutation",
@@ -79,7 +103,34 @@ class HipMoESortChunks(OpImpl):
 
     def __call__(self, input, split_sizes, sorted_idxs, probs=None):
         require_cuda(input, split_sizes, sorted_idxs, probs)
+        if split_sizes.dim() != 1 or sorted_idxs.dim() != 1:
+            raise ValueError("moe_sort_chunks expects 1-D split_sizes and sorted_idxs.")
+        if split_sizes.numel() != sorted_idxs.numel():
+            raise ValueError(
+                f"moe_sort_chunks: {sorted_idxs.numel()} chunk ids for "
+                f"{split_sizes.numel()} chunks; sorted_idxs must order every chunk once."
+            )
+        if probs is not None and probs.shape[0] != input.shape[0]:
+            raise ValueError("moe_sort_chunks: probs must have one entry per input row.")
+        if checks.enabled():
+            _check_chunks(input.shape[0], split_sizes, sorted_idxs)
         return _SortChunks.apply(input, probs, split_sizes, sorted_idxs)
+
+
+def _check_chunks(rows, sizes, order):
+    """What torch.split / the chunk loop of the reference reject
+    (native/moe_permutation.py:117-119): sizes that do not cover the rows
+    exactly, negative sizes, or an order that is not a permutation."""
+    C = sizes.numel()
+    total = int(sizes.sum()) if C else 0
+    if total != rows or (C and int(sizes.min()) < 0):
+        raise ValueError(f"moe_sort_chunks: split_sizes sum to {total}, the input has {rows} rows.")
+    seen = torch.zeros(C, dtype=torch.int64, device=order.device)
+    valid = bool(((order >= 0) & (order < C)).all()) if C else True
+    if valid and C:
+        seen.index_add_(0, order.long(), torch.ones_like(order, dtype=torch.int64))
+    if not valid or not bool((seen == 1).all()):
+        raise ValueError("moe_sort_chunks: sorted_idxs must be a permutation of the chunk ids.")
 
 
 def _sort_chunks(x, probs, sizes, order):
