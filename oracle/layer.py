@@ -73,17 +73,30 @@ def moe_layer(hidden, logits, w1, w2, cfg: RoutingConfig, *, expert_bias=None,
     given, ``w1``/``w2`` are ignored. ``shared``: optional callable on hidden.
     """
     probs, routing_map, ids = route(logits, cfg, expert_bias)
+    return moe_layer_routed(hidden, probs, routing_map, ids, w1, w2, shared=shared, fp8=fp8,
+                            trace=trace)
+
+
+def moe_layer_routed(hidden, probs, routing_map, ids, w1, w2, *, shared=None, fp8=None,
+                     trace: bool = False, stacked_grad: bool = False):
+    """Steps 2-6 from a routing result: probs [T, E], routing_map [T, E] (bool),
+    ids [T, k]. Every output row depends only on its own token's routing, so a
+    caller may pass a subset of the tokens, and only the experts that subset
+    uses (columns of probs / routing_map, ids renumbered in the same order).
+    ``stacked_grad``: see ``native_providers.grouped_matmul.grouped_matmul``."""
     counts = routing_map.sum(dim=0).long()
     perm = permute(hidden, routing_map, probs=probs, expert_indices=ids)
+    sg = dict(stacked_grad=stacked_grad)
     if fp8 is None:
-        fc1 = grouped_matmul(perm.tokens, w1, counts)
+        fc1 = grouped_matmul(perm.tokens, w1, counts, **sg)
     else:
-        fc1 = grouped_matmul_fp8(perm.tokens, fp8["q1"], fp8["s1"], counts, master=fp8.get("m1"))
+        fc1 = grouped_matmul_fp8(perm.tokens, fp8["q1"], fp8["s1"], counts, master=fp8.get("m1"),
+                                 **sg)
     act = swiglu_probs(fc1, perm.probs)
     if fp8 is None:
-        fc2 = grouped_matmul(act, w2, counts)
+        fc2 = grouped_matmul(act, w2, counts, **sg)
     else:
-        fc2 = grouped_matmul_fp8(act, fp8["q2"], fp8["s2"], counts, master=fp8.get("m2"))
+        fc2 = grouped_matmul_fp8(act, fp8["q2"], fp8["s2"], counts, master=fp8.get("m2"), **sg)
     combined = unpermute(
         MoEPermutation(fc2, None, perm.row_indices, perm.expert_indices), hidden.shape
     )

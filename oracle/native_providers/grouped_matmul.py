@@ -26,7 +26,13 @@ def counts_list(tokens_per_expert) -> list[int]:
     return [int(c) for c in tokens_per_expert]
 
 
-def grouped_matmul(x, weight, tokens_per_expert, *, trans_b: bool = False):
+def grouped_matmul(x, weight, tokens_per_expert, *, trans_b: bool = False,
+                   stacked_grad: bool = False):
+    """``stacked_grad=False`` keeps the reference's autograd structure: one
+    ``weight[e]`` per expert, whose backward allocates a full-size gradient
+    buffer per expert (what the CPU baseline times). ``True`` takes the expert
+    slices from one ``weight.unbind(0)``: the same gradient values with one
+    full-size buffer, for checks of layers with many experts."""
     if weight.ndim != 3:
         raise ValueError(
             "grouped_matmul expects weight with shape (experts, in_features, out_features)."
@@ -36,9 +42,11 @@ def grouped_matmul(x, weight, tokens_per_expert, *, trans_b: bool = False):
         raise ValueError("tokens_per_expert must match the number of expert weight slices.")
     pieces = []
     begin = 0
+    slices = weight.unbind(0) if stacked_grad else None
     for expert, n in enumerate(counts):
         if n:
-            w = weight[expert].t() if trans_b else weight[expert]
+            w = slices[expert] if stacked_grad else weight[expert]
+            w = w.t() if trans_b else w
             pieces.append(x[begin:begin + n].matmul(w))
         begin += n
     if pieces:

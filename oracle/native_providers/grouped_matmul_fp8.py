@@ -33,11 +33,12 @@ class _DequantWithMasterGrad(torch.autograd.Function):
         return grad, None
 
 
-def grouped_matmul_fp8(x, qweight, scale, tokens_per_expert, *, master=None):
+def grouped_matmul_fp8(x, qweight, scale, tokens_per_expert, *, master=None,
+                       stacked_grad=False):
     deq = dequantize_experts(qweight, scale)
     if master is not None:
         deq = _DequantWithMasterGrad.apply(master, deq)
-    return grouped_matmul(x, deq, tokens_per_expert, trans_b=True)
+    return grouped_matmul(x, deq, tokens_per_expert, trans_b=True, stacked_grad=stacked_grad)
 
 
 @register_op(op_name="grouped_matmul_fp8", impl_name="torch_grouped_matmul_fp8",

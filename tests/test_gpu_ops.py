@@ -508,6 +508,126 @@ def test_permutation_kats(hip_ops):
         assert o.cpu().float().flatten().tolist() == [1.0, 2.0]
 
 
+def test_sort_chunks_kats(hip_ops):
+    """tests/models/test_moe_permutation.py:125-130 and :133-151 (an empty chunk, probs,
+    gradients, and the inverse order restoring the input), on the GPU."""
+    tokens = torch.tensor([[10.0], [20.0], [30.0]], device=DEV)
+    out, _ = hip_ops.moe_sort_chunks(tokens, torch.tensor([1, 2], device=DEV),
+                                     torch.tensor([1, 0], device=DEV))
+    assert out.cpu().tolist() == [[20.0], [30.0], [10.0]]
+    for n in (0, 3):
+        tokens = torch.tensor([[10.0], [20.0], [30.0]], device=DEV)[:n].requires_grad_()
+        probs = torch.tensor([0.1, 0.2, 0.3], device=DEV)[:n].requires_grad_()
+        sizes = torch.tensor([2, 0, 1] if n else [0, 0, 0], device=DEV)
+        order = torch.tensor([2, 0, 1], device=DEV)
+        output, weights = hip_ops.moe_sort_chunks(tokens, sizes, order, probs=probs)
+        rows = torch.tensor([2, 0, 1] if n else [], dtype=torch.long, device=DEV)
+        assert torch.equal(output, tokens[rows])
+        restored, _ = hip_ops.moe_sort_chunks(output, sizes[order], order.argsort())
+        assert torch.equal(restored, tokens)
+        (output * weights[:, None]).sum().backward()
+        assert torch.equal(tokens.grad.flatten(), probs.detach())
+        assert torch.equal(probs.grad, tokens.detach().flatten())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("C,H,max_rows", [(8, 256, 300), (128, 2048, 96), (33, 5000, 40),
+                                          (4096, 64, 12), (64, 1, 50)])
+def test_sort_chunks_matches_oracle(hip_ops, dtype, C, H, max_rows):
+    """Random chunk sizes (empty chunks included) and orders, among them the EP
+    exchange's (rank, expert) -> (expert, rank) transpose; rows, probs and both
+    gradients bit-exact against the oracle (a pure data movement)."""
+    g = torch.Generator().manual_seed(C + H)
+    sizes = torch.randint(0, max_rows + 1, (C,), generator=g)
+    sizes[C // 2] = 0
+    if C == 128:  # 8 ranks x 16 local experts, regrouped by expert
+        order = torch.arange(C).view(8, 16).t().reshape(-1)
+    else:
+        order = torch.randperm(C, generator=g)
+    rows = int(sizes.sum())
+    x = torch.randn(rows, H, generator=g).to(dtype)
+    if H == 1:
+        x = x.view(rows)
+    p = torch.rand(rows, generator=g)
+    gx = torch.randn(x.shape, generator=g).to(dtype)
+    gp = torch.randn(rows, generator=g)
+    xr, pr = x.clone().requires_grad_(), p.clone().requires_grad_()
+    out_r, outp_r = o_perm.sort_chunks(xr, sizes, order, probs=pr)
+    torch.autograd.backward([out_r, outp_r], [gx, gp])
+    xd, pd = x.to(DEV).requires_grad_(), p.to(DEV).requires_grad_()
+    out_d, outp_d = hip_ops.moe_sort_chunks(xd, sizes.to(DEV), order.to(DEV), probs=pd)
+    torch.autograd.backward([out_d, outp_d], [gx.to(DEV), gp.to(DEV)])
+    assert torch.equal(out_d.cpu(), out_r.detach())
+    assert torch.equal(outp_d.cpu(), outp_r.detach())
+    assert torch.equal(xd.grad.cpu(), xr.grad)
+    assert torch.equal(pd.grad.cpu(), pr.grad)
+    # the inverse order restores the input
+    back, _ = hip_ops.moe_sort_chunks(out_d.detach(), sizes[order].to(DEV), order.argsort().to(DEV))
+    assert torch.equal(back.cpu(), x)
+
+
+def test_sort_chunks_rejects_inconsistent_metadata(hip_ops):
+    from torchturbo_amd import checks
+
+    x = torch.randn(10, 4, device=DEV)
+    with pytest.raises(ValueError, match="chunk ids"):
+        hip_ops.moe_sort_chunks(x, torch.tensor([5, 5], device=DEV), torch.tensor([0], device=DEV))
+    with pytest.raises(ValueError, match="input device"):
+        hip_ops.moe_sort_chunks(x, torch.tensor([5, 5]), torch.tensor([1, 0], device=DEV))
+    with checks.checking():
+        with pytest.raises(ValueError, match="sum to 9"):
+            hip_ops.moe_sort_chunks(x, torch.tensor([5, 4], device=DEV),
+                                    torch.tensor([1, 0], device=DEV))
+        with pytest.raises(ValueError, match="permutation"):
+            hip_ops.moe_sort_chunks(x, torch.tensor([5, 5], device=DEV),
+                                    torch.tensor([1, 1], device=DEV))
+        out, _ = hip_ops.moe_sort_chunks(x, torch.tensor([6, 4], device=DEV),
+                                         torch.tensor([1, 0], device=DEV))
+        assert torch.equal(out, torch.cat([x[6:], x[:6]]))
+
+
+def test_routing_ids_out_of_range_or_repeated(hip_ops):
+    """Bad routing input. With checks on: ValueError, as the reference's gather and
+    top-k checks raise (ops/moe.py:62-65, native/moe_permutation.py:52-56). With checks
+    off: the rejected slots get row -1, no packed row and no count; every accepted slot
+    keeps the reference's expert-major, token-ascending row."""
+    from torchturbo_amd import checks
+
+    T, H, E, k = 64, 32, 8, 3
+    ids = distinct_ids(T, E, k, seed=5)
+    rmap = torch.zeros(T, E, dtype=torch.bool).scatter(1, ids, True)
+    x = torch.randn(T, H)
+    bad = ids.clone()
+    bad[5, 1] = E          # out of range
+    bad[9, 0] = -1         # out of range
+    bad[12, 2] = bad[12, 0]  # repeated within the token
+    with checks.checking():
+        with pytest.raises(ValueError, match="3 of 192 slots"):
+            hip_ops.moe_permutation(x.to(DEV), rmap.to(DEV), expert_indices=bad.to(DEV))
+        other = ids.clone()
+        free = [e for e in range(E) if e not in ids[3].tolist()][0]
+        other[3, 0] = free   # valid, distinct, but not what routing_map selects
+        with pytest.raises(ValueError, match="disagree for 1 of 64 tokens"):
+            hip_ops.moe_permutation(x.to(DEV), rmap.to(DEV), expert_indices=other.to(DEV))
+        ok = hip_ops.moe_permutation(x.to(DEV), rmap.to(DEV), expert_indices=ids.to(DEV))
+        assert int(ok.tokens_per_expert.sum()) == T * k
+    got = hip_ops.moe_permutation(x.to(DEV), rmap.to(DEV), expert_indices=bad.to(DEV))
+    rows = got.row_indices.cpu()
+    rejected = {(5, 1), (9, 0), (12, 2)}
+    accepted = sorted((int(bad[t, j]), t, j) for t in range(T) for j in range(k)
+                      if (t, j) not in rejected)
+    expect = torch.full((T, k), -1, dtype=torch.int32)
+    for r, (_, t, j) in enumerate(accepted):
+        expect[t, j] = r
+    assert torch.equal(rows, expect)
+    assert int(got.tokens_per_expert.sum()) == T * k - 3
+    assert torch.equal(got.tokens[:len(accepted)].cpu(), x[[t for _, t, _ in accepted]])
+    # the combine skips rejected slots: token t gets (accepted slots of t) * x[t]
+    out = hip_ops.moe_unpermutation(got, torch.Size([T, H])).cpu()
+    n_ok = torch.tensor([sum((t, j) not in rejected for j in range(k)) for t in range(T)])
+    assert torch.equal(out, x * n_ok[:, None].float())
+
+
 def test_permutation_empty_and_zero_weight(hip_ops):
     tokens = torch.empty(0, 4, device=DEV, requires_grad=True)
     probs = torch.empty(0, 3, device=DEV, requires_grad=True)
@@ -681,6 +801,70 @@ def test_grouped_matmul_integer_exact(hip_ops):
     assert torch.equal(y.cpu(), yr.to(torch.bfloat16))
     assert torch.equal(xd.grad.cpu(), xr.grad.to(torch.bfloat16))
     assert torch.equal(wd.grad.cpu(), wr.grad.to(torch.bfloat16))
+
+
+def _zipf_counts(E, M, seed, empty=(3, 17)):
+    """Zipf(1.1)-skewed expert loads summing to M, with some empty experts."""
+    g = torch.Generator().manual_seed(seed)
+    rank = torch.randperm(E, generator=g).double() + 1.0
+    p = rank.pow(-1.1)
+    p /= p.sum()
+    c = (p * M).floor().long()
+    for e in empty:
+        c[e] = 0
+    c[int(rank.argmin())] += M - int(c.sum())  # the top expert takes the remainder
+    assert int(c.sum()) == M and int(c.min()) >= 0
+    return c
+
+
+# Shapes of the Qwen3-30B-A3B layer's two GEMMs (fc1: K 2048 -> N 1536, fc2: K 768 ->
+# N 2048), tens of thousands of rows, Zipf loads with empty experts. Each launch has far
+# more 256x256 output tiles than the GPU has compute units, so every persistent block
+# walks many tiles (tile switch, cross-tile prefetch, XCD remap); mean expert loads above
+# 512 rows take the four-stage weight-gradient kernel, at most 512 the persistent
+# weight-gradient kernel with its ticket queues (many tickets per block).
+MANY_TILES = [
+    (torch.bfloat16, False, 64, 65536, 2048, 1536),
+    (torch.bfloat16, True, 64, 65536, 2048, 1536),
+    (torch.bfloat16, False, 64, 65536, 768, 2048),
+    (torch.bfloat16, True, 128, 32768, 768, 2048),
+    (torch.bfloat16, False, 128, 32768, 2048, 1536),
+    (torch.float16, False, 128, 49152, 2048, 1536),
+    (torch.bfloat16, False, 64, 40000, 2000, 1000),  # reduction tails: K, N not multiples of 64
+]
+
+
+@pytest.mark.parametrize("dtype,trans_b,E,M,K,N", MANY_TILES,
+                         ids=lambda v: str(v).replace("torch.", ""))
+def test_grouped_matmul_many_tiles(hip_ops, dtype, trans_b, E, M, K, N):
+    """fwd, dgrad and wgrad against per-expert fp32 products (torch, same device)."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    counts = _zipf_counts(E, M, seed=E + K + N)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    slots = int(sum((int(c) + 255) // 256 for c in counts)) * ((N + 255) // 256)
+    assert slots > 2 * cus, (slots, cus)  # several output tiles per persistent block
+    g = torch.Generator(device=DEV).manual_seed(7)
+    x = torch.randn(M, K, generator=g, device=DEV).to(dtype).requires_grad_()
+    wshape = (E, N, K) if trans_b else (E, K, N)
+    w = (torch.randn(*wshape, generator=g, device=DEV) * 0.05).to(dtype).requires_grad_()
+    dy = torch.randn(M, N, generator=g, device=DEV).to(dtype)
+    y = hip_ops.grouped_matmul(x, w, counts.to(DEV), trans_b=trans_b)
+    y.backward(dy)
+    xs = torch.split(x.detach().float(), counts.tolist())
+    ds = torch.split(dy.float(), counts.tolist())
+    wf = w.detach().float()
+    yr, dxr, dwr = [], [], torch.zeros(wshape, device=DEV)
+    for e in range(E):
+        we = wf[e].t() if trans_b else wf[e]  # [K, N]
+        yr.append(xs[e] @ we)
+        dxr.append(ds[e] @ we.t())
+        dwe = xs[e].t() @ ds[e]  # [K, N]
+        dwr[e] = dwe.t() if trans_b else dwe
+    for a, b, name in ((y, torch.cat(yr), "y"), (x.grad, torch.cat(dxr), "dx"), (w.grad, dwr, "dw")):
+        mx, mean = rel_errors(a.float(), b)
+        assert mx <= 1e-2 and mean <= 2e-3, f"{name}: {mx:.3e} {mean:.3e}"
+    for e in (counts == 0).nonzero().flatten().tolist():
+        assert torch.count_nonzero(w.grad[e]) == 0
 
 
 # ---------------------------------------------------------------------------
