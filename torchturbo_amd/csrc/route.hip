@@ -1291,25 +1291,30 @@ extern "C" size_t tt_route_index_rejected_offset(int64_t num_tokens, int32_t num
   return (size_t)(nb * num_experts + num_experts + nb) * sizeof(int);
 }
 
-extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
-                              int32_t num_experts, const void* probs_dense, int probs_dtype,
-                              int32_t* row_indices, int32_t* token_of_row, void* packed_probs,
-                              int64_t* tokens_per_expert, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+namespace {
+
+int route_index_args(int64_t num_tokens, int32_t topk, int32_t num_experts,
+                     const void* probs_dense, void* packed_probs, int probs_dtype) {
   TT_REQUIRE(num_tokens >= 0 && num_tokens * (int64_t)topk < (1ll << 31),
              "route_index: T * k must fit in int32");
   TT_REQUIRE(num_experts >= 1 && num_experts <= 2048, "route_index: num_experts must be in [1, 2048]");
   TT_REQUIRE(topk >= 1 && topk <= 64, "route_index: topk must be in [1, 64]");
-  TT_REQUIRE(workspace_bytes >= tt_route_index_workspace(num_tokens, num_experts),
-             "route_index: workspace too small");
   if (probs_dense != nullptr && packed_probs != nullptr)
     TT_REQUIRE(float_dtype(probs_dtype), "route_index: unsupported probs dtype %d", probs_dtype);
-  hipStream_t s = S(stream);
+  return TT_OK;
+}
+
+// The three routing-index kernels over a scratch area laid out as the
+// workspace of tt_route_index (bc | totals | bad); the rejected-slot count
+// goes to bad_total.
+int route_index_run(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
+                    int32_t num_experts, const void* probs_dense, int probs_dtype,
+                    int32_t* row_indices, int32_t* token_of_row, void* packed_probs,
+                    int64_t* tokens_per_expert, int* area, int* bad_total, hipStream_t s) {
   const int nb = (int)((num_tokens + kIdxBlock - 1) / kIdxBlock);
-  int* bc = static_cast<int*>(workspace);
+  int* bc = area;
   int* totals = bc + (int64_t)nb * num_experts;
   int* bad = totals + num_experts;
-  int* bad_total = bad + nb;
   if (num_tokens == 0) {
     // Counts are all zero; a one-wave scan over zero blocks writes them.
     hipLaunchKernelGGL(route_scan_kernel, dim3(num_experts), dim3(64), 0, s, bc, 0, num_experts,
@@ -1344,6 +1349,26 @@ extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens,
   else TT_RANK(64);
 #undef TT_RANK
   return tt_check_launch("route_rank");
+}
+
+}  // namespace
+
+extern "C" int tt_route_index(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
+                              int32_t num_experts, const void* probs_dense, int probs_dtype,
+                              int32_t* row_indices, int32_t* token_of_row, void* packed_probs,
+                              int64_t* tokens_per_expert, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const int rc = route_index_args(num_tokens, topk, num_experts, probs_dense, packed_probs,
+                                  probs_dtype);
+  if (rc != TT_OK) return rc;
+  TT_REQUIRE(workspace_bytes >= tt_route_index_workspace(num_tokens, num_experts),
+             "route_index: workspace too small");
+  int* area = static_cast<int*>(workspace);
+  int* bad_total = reinterpret_cast<int*>(
+      static_cast<char*>(workspace) + tt_route_index_rejected_offset(num_tokens, num_experts));
+  return route_index_run(expert_indices, num_tokens, topk, num_experts, probs_dense, probs_dtype,
+                         row_indices, token_of_row, packed_probs, tokens_per_expert, area,
+                         bad_total, S(stream));
 }
 
 extern "C" size_t tt_router_loss_workspace(int64_t num_tokens, int32_t num_experts) {
