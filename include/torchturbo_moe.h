@@ -135,6 +135,21 @@ int tt_route_index(const int64_t* expert_indices, int64_t num_tokens, int32_t to
                    int64_t* tokens_per_expert, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* tt_route_index without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops). No
+ * counterpart in the reference. The histograms live in a fixed 1 MiB device
+ * array of the library (one per GPU, kept until the process ends), so the
+ * call allocates nothing; it rejects problems whose
+ * tt_route_index_workspace(T, E) exceeds 1 MiB (e.g. E = 128 up to about
+ * 520k tokens) with TT_ERR_INVALID. Outputs are those of tt_route_index; the
+ * rejected-slot count goes to *rejected (device int32) when non-NULL. All
+ * calls on one GPU share the array: calls that overlap on a GPU (several
+ * streams or host threads) race and must be serialised by the caller. */
+int tt_route_index_noalloc(const int64_t* expert_indices, int64_t num_tokens, int32_t topk,
+                           int32_t num_experts, const void* probs_dense, int probs_dtype,
+                           int32_t* row_indices, int32_t* token_of_row, void* packed_probs,
+                           int64_t* tokens_per_expert, int32_t* rejected, void* stream);
+
 /* ---- Permute / unpermute -------------------------------------------------
  * Token rows -> packed rows: packed[row_indices[t, j]] = tokens[t].
  * Replaces the index_select of native moe_permutation.py:43 (and TE

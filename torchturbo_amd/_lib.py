@@ -42,6 +42,7 @@ _PROTOS: dict[str, list] = {
     "tt_router_loss_fwd": [P, c_int, I64, I32, I32, I32, P, P, P, P, P, c_size_t, P],
     "tt_router_loss_bwd": [P, c_int, I64, I32, I32, P, P, P, P, P],
     "tt_route_index": [P, I64, I32, I32, P, c_int, P, P, P, P, P, c_size_t, P],
+    "tt_route_index_noalloc": [P, I64, I32, I32, P, c_int, P, P, P, P, P, P],
     "tt_permute_scatter": [P, c_int, I64, I64, I32, P, P, P],
     "tt_unpermute_gather": [P, c_int, I64, I64, I32, P, P, P, c_int, I32, P, P],
     "tt_unpermute_gather_bwd": [P, P, c_int, I64, I64, I32, P, P, P, c_int, I32, P, P, P],

@@ -14,6 +14,8 @@
 // lanes below it), so the order is the token order and is reproducible.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -1506,4 +1508,77 @@ extern "C" int tt_router_gate_fwd(const void* x, const void* weight, int in_dtyp
   }
 #undef TT_GATE_N
 #undef TT_GATE
+}
+
+// ---------------------------------------------------------------------------
+// Routing index without a caller workspace.
+// ---------------------------------------------------------------------------
+// The per-block histograms, expert totals and rejected-slot counts of
+// tt_route_index_noalloc live in this fixed array instead of a workspace:
+// one copy per GPU, held until the process ends. Every kernel writes each
+// entry it later reads, so nothing needs clearing between calls. All calls
+// on one GPU share the array: calls that overlap on a GPU (other streams or
+// host threads) race.
+constexpr size_t kRouteScratchBytes = 1u << 20;
+static __device__ __align__(256) unsigned char scratch[kRouteScratchBytes];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+void* g_scratch_ptr[kScratchDevices];
+hipError_t g_scratch_err[kScratchDevices];
+std::once_flag g_scratch_once[kScratchDevices];
+
+// Device address of the current GPU's copy of `scratch`, looked up once per
+// device with that device current. In host code the array's name only stands
+// for the symbol; kernels get this address.
+int route_scratch(void** out) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess) {
+    tt_set_error("route_index_noalloc: hipGetDevice: %s", hipGetErrorString(ge));
+    return TT_ERR_HIP;
+  }
+  TT_REQUIRE(dev >= 0 && dev < kScratchDevices, "route_index_noalloc: device %d unsupported", dev);
+  std::call_once(g_scratch_once[dev], [dev]() {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+  });
+  if (g_scratch_err[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr) {
+    tt_set_error("route_index_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                 hipGetErrorString(g_scratch_err[dev]));
+    return TT_ERR_HIP;
+  }
+  *out = g_scratch_ptr[dev];
+  return TT_OK;
+}
+
+}  // namespace
+
+extern "C" int tt_route_index_noalloc(const int64_t* expert_indices, int64_t num_tokens,
+                                      int32_t topk, int32_t num_experts, const void* probs_dense,
+                                      int probs_dtype, int32_t* row_indices,
+                                      int32_t* token_of_row, void* packed_probs,
+                                      int64_t* tokens_per_expert, int32_t* rejected,
+                                      void* stream) {
+  const int rc = route_index_args(num_tokens, topk, num_experts, probs_dense, packed_probs,
+                                  probs_dtype);
+  if (rc != TT_OK) return rc;
+  const size_t need = tt_route_index_workspace(num_tokens, num_experts);
+  TT_REQUIRE(need <= kRouteScratchBytes,
+             "route_index_noalloc: %lld tokens over %d experts need %zu bytes of scratch, "
+             "more than the fixed %zu; use tt_route_index with a workspace",
+             (long long)num_tokens, num_experts, need, kRouteScratchBytes);
+  void* area = nullptr;
+  const int rs = route_scratch(&area);
+  if (rs != TT_OK) return rs;
+  int* bad_total = rejected != nullptr
+                       ? reinterpret_cast<int*>(rejected)
+                       : reinterpret_cast<int*>(static_cast<char*>(area) +
+                                                tt_route_index_rejected_offset(num_tokens,
+                                                                               num_experts));
+  return route_index_run(expert_indices, num_tokens, topk, num_experts, probs_dense, probs_dtype,
+                         row_indices, token_of_row, packed_probs, tokens_per_expert,
+                         static_cast<int*>(area), bad_total, S(stream));
 }
