@@ -692,8 +692,10 @@ __device__ __forceinline__ uint32_t fragk64(int r0, int s, int lane) {
 // output width are given an offset past the resource. AUX is the stores'
 // cache policy: 2 (streaming) for weight gradients, which nothing in the
 // step reads back (5 % faster on DeepSeek-V3's write-bound weight
-// gradients); 0 for activations, which the next kernel reads.
-template <int ET, int AUX>
+// gradients); 0 for activations, which the next kernel reads. The wave's
+// 32-row block mi starts ROWSTEP * mi rows below ri; only its first NMI
+// blocks are stored (the others lie past the expert's rows).
+template <int ET, int AUX, int ROWSTEP, int NMI>
 __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], const TileDesc& t,
                                                     int64_t ri, int64_t cj, lds_char* region) {
   // Lane index computed here (volatile, so neither it nor what derives from
@@ -712,7 +714,7 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
   const int r_l = lane & 31, h = lane >> 5;
   const int rr = lane >> 3, ch = lane & 7;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < NMI; ++mi)
 #pragma unroll
     for (int nh = 0; nh < 2; ++nh) {
 #pragma unroll
@@ -741,7 +743,7 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
       for (int q = 0; q < 4; ++q) {
         const int r = 8 * q + rr;
         const uint4 v = read_k(region, (uint32_t)(r * 128 + ((ch ^ ((r >> 1) & 7)) << 4)));
-        const uint32_t off = col_ok ? (uint32_t)(32 * mi + r) * row_bytes + (uint32_t)col * 2u
+        const uint32_t off = col_ok ? (uint32_t)(ROWSTEP * mi + r) * row_bytes + (uint32_t)col * 2u
                                     : DM_OOB;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (int)off, 0, AUX);
       }
@@ -1002,10 +1004,18 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
                        (uint32_t)(8 * wave + (q & 7)) * 1024u);
   };
 
+  // A fragments. wgrad (MN-major A): wave row wm owns tile rows 128 wm ..
+  // 128 wm + 127, 32-row block mi at +32 mi. fwd / dgrad (K-major A): the
+  // blocks of the two wave rows interleave, wave row wm owning tile rows
+  // 64 mi + 32 wm .. + 31, so the rows an expert's last (partial) tile holds
+  // spread evenly over both wave rows and the blocks past them can be skipped.
+  constexpr uint32_t A_MI = WG ? 4096u : 8192u;  // LDS bytes between a wave's A blocks
+  constexpr int EPI_ROWS = WG ? 32 : 64;         // output rows between a wave's blocks
+  const int a_row0 = WG ? wm * WT : 32 * wm;
   uint32_t a_k[4], b_k[4], a_mn[FM], b_mn[FN];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    a_k[s] = fragk64(wm * WT, s, lane);
+    a_k[s] = fragk64(a_row0, s, lane);
     b_k[s] = fragk64(wn * WT, s, lane) + P_OPND;
   }
 #pragma unroll
@@ -1027,12 +1037,15 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     if constexpr (Lay::B_K) asm volatile("" : "+v"(bo));
     else asm volatile("" : "+v"(bm[0]), "+v"(bm[1]), "+v"(bm[2]), "+v"(bm[3]));
   };
-  auto frag = [&](lds_char* stg, int s, int i, uint4 (&fa)[FM], uint4 (&fb)[FN]) {
-    if (i < FM)
-      fa[i] = Lay::A_K ? read_k(stg, ao + i * 4096) : read_mn(stg, am[i] + s * 8192);
+  // Fragment i of k-step s for a tile whose waves multiply MV of their four
+  // 32-row blocks: A blocks 0 .. MV - 1, then the four B blocks.
+  auto frag = [&](auto mv_c, lds_char* stg, int s, int i, uint4 (&fa)[FM], uint4 (&fb)[FN]) {
+    constexpr int MV = decltype(mv_c)::value;
+    if (i < MV)
+      fa[i] = Lay::A_K ? read_k(stg, ao + i * A_MI) : read_mn(stg, am[i] + s * 8192);
     else
-      fb[i - FM] = Lay::B_K ? read_k(stg, bo + (i - FM) * 4096)
-                            : read_mn(stg, bm[i - FM] + s * 8192);
+      fb[i - MV] = Lay::B_K ? read_k(stg, bo + (i - MV) * 4096)
+                            : read_mn(stg, bm[i - MV] + s * 8192);
   };
   auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
     acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
@@ -1042,16 +1055,22 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   auto stage = [&](int g) { return lds + (g & 1) * P_STAGE; };
   uint4 a0[FM], b0[FN], a1[FM], b1[FN];
 
-  // One k-tile: k-steps 0-2 multiply while reading the next k-step (and
-  // k-steps 0 and 1 load the B half of k-tile kt + 1 into the other stage,
-  // one load every fourth MFMA slot); then wait for k-tile kt + 1 (the only
-  // loads in flight), barrier (every wave is past its reads of this stage),
-  // and k-step 3 multiplies while reading k-step 0 of k-tile kt + 1 and
-  // loading the A half of k-tile kt + 2 into this stage (every other slot).
+  // One k-tile of a tile whose waves multiply MV (4, 2 or 1) of their 32-row
+  // blocks, NM = 4 MV MFMAs per k-step: k-steps 0-2 multiply while reading
+  // the next k-step's fragments (and k-steps 0 and 1 load the B half of
+  // k-tile kt + 1 into the other stage, spread over the MFMA slots); then wait
+  // for k-tile kt + 1 (the only loads in flight), barrier (every wave is past
+  // its reads of this stage), and k-step 3 multiplies while reading k-step 0
+  // of k-tile kt + 1 and loading the A half of k-tile kt + 2 into this stage.
   // Issuing a k-tile's 16 loads in one k-step backs up the vector memory
-  // path and stalls the MFMAs behind it.
-  auto step = [&](int kt, int g, auto last_c) {
+  // path and stalls the MFMAs behind it. The loads are the same in every
+  // variant: rows past an expert's end read as zeros without memory traffic.
+  auto step = [&](int kt, int g, auto last_c, auto mv_c) {
     constexpr bool LAST = decltype(last_c)::value;
+    constexpr int MV = decltype(mv_c)::value;
+    constexpr int NM = MV * FN;       // MFMAs per k-step
+    constexpr int NF = MV + FN;       // fragment reads per k-step
+    constexpr int LS = NM / 4;        // MFMA slots per B load (k-steps 0, 1)
     lds_char* const cur = stage(g);
     lds_char* const nxt = stage(g + 1);
     const int k1 = kt + 1, k2 = kt + 2;
@@ -1066,13 +1085,17 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     for (int s = 0; s < 3; ++s) {
       refresh(s + 1);
 #pragma unroll
-      for (int i = 0; i < FM * FN; ++i) {
+      for (int i = 0; i < NM; ++i) {
         if (s & 1) mfma(i, a1, b1); else mfma(i, a0, b0);
-        if (i < FM + FN) {
-          if (s & 1) frag(cur, s + 1, i, a0, b0); else frag(cur, s + 1, i, a1, b1);
+        if (i < NF) {
+          if (s & 1) frag(mv_c, cur, s + 1, i, a0, b0); else frag(mv_c, cur, s + 1, i, a1, b1);
         }
-        if (s <= 1 && (i & 3) == 1) issue_one(nxt, kr1, to_next1, 8 + 4 * s + (i >> 2));
+        if (s <= 1 && i % LS == (LS > 1 ? 1 : 0)) issue_one(nxt, kr1, to_next1, 8 + 4 * s + i / LS);
         __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = NM; i < NF; ++i) {  // one MFMA per wave row: a read left over
+        if (s & 1) frag(mv_c, cur, s + 1, i, a0, b0); else frag(mv_c, cur, s + 1, i, a1, b1);
       }
     }
     TT_WAIT_VMCNT(0);
@@ -1096,12 +1119,20 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     }
     refresh(0);
 #pragma unroll
-    for (int i = 0; i < FM * FN; ++i) {
+    for (int i = 0; i < NM; ++i) {
       mfma(i, a1, b1);
-      if (!LAST && i < FM + FN) frag(nxt, 0, i, a0, b0);
-      if (i & 1) issue_one(cur, kr2, to_next2, i >> 1);
+      if (!LAST && i < NF) frag(mv_c, nxt, 0, i, a0, b0);
+      if constexpr (NM >= 8) {
+        if (i % (NM / 8) == (NM / 8 - 1)) issue_one(cur, kr2, to_next2, i / (NM / 8));
+      } else {
+        issue_one(cur, kr2, to_next2, 2 * i);
+        issue_one(cur, kr2, to_next2, 2 * i + 1);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int i = NM; i < NF; ++i)
+      if (!LAST) frag(mv_c, nxt, 0, i, a0, b0);
   };
 
   // k-tile 0 whole and the A half of k-tile 1 (its B half goes out in the
@@ -1114,22 +1145,39 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   __builtin_amdgcn_s_barrier();
   refresh(0);
 #pragma unroll
-  for (int i = 0; i < FM + FN; ++i) frag(stage(0), 0, i, a0, b0);
+  for (int i = 0; i < FM + FN; ++i) frag(std::integral_constant<int, FM>{}, stage(0), 0, i, a0, b0);
 
   lds_char* const epi = (lds_char*)epi_raw + wave * P_EPI;
-  int g = 0;
-  for (;;) {
+  // One output tile with MV blocks per wave: its k-tiles, then the epilogue
+  // (rounds of the wave's blocks that hold rows).
+  auto run_tile = [&](auto mv_c, int& g) {
+    constexpr int MV = decltype(mv_c)::value;
 #pragma unroll
-    for (int mi = 0; mi < FM; ++mi)
+    for (int mi = 0; mi < MV; ++mi)
 #pragma unroll
       for (int ni = 0; ni < FN; ++ni)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
-    for (int kt = 0; kt < nkt_c - 1; ++kt, ++g) step(kt, g, std::false_type{});
-    step(nkt_c - 1, g, std::true_type{});
+    for (int kt = 0; kt < nkt_c - 1; ++kt, ++g) step(kt, g, std::false_type{}, mv_c);
+    step(nkt_c - 1, g, std::true_type{}, mv_c);
     ++g;
     __builtin_amdgcn_sched_barrier(0);
-    store_wave_tile_p64<ET, WG ? 2 : 0>(acc, tc, tc.i0 + wm * WT, tc.j0 + wn * WT, epi);
+    store_wave_tile_p64<ET, WG ? 2 : 0, EPI_ROWS, MV>(acc, tc, tc.i0 + a_row0, tc.j0 + wn * WT,
+                                                      epi);
+  };
+  int g = 0;
+  for (;;) {
+    // Blocks of 32 rows that hold rows of the expert, per wave row (the
+    // interleaved blocks of a tile with b of them: ceil(b / 2)).
+    int mv = 4;
+    if constexpr (!WG) {
+      const int64_t left = tc.nrows - tc.i0;
+      const int nb32 = left >= DM_BM ? 8 : (int)((left + 31) / 32);
+      mv = nb32 <= 2 ? 1 : (nb32 <= 4 ? 2 : 4);
+    }
+    if (mv == 4) run_tile(std::integral_constant<int, 4>{}, g);
+    else if (mv == 2) run_tile(std::integral_constant<int, 2>{}, g);
+    else run_tile(std::integral_constant<int, 1>{}, g);
     if (!has_next) break;
     tc = tn;
     nkt_c = nkt_n;
@@ -1150,7 +1198,8 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     ++n;
     refresh(0);
 #pragma unroll
-    for (int i = 0; i < FM + FN; ++i) frag(stage(g), 0, i, a0, b0);
+    for (int i = 0; i < FM + FN; ++i)
+      frag(std::integral_constant<int, FM>{}, stage(g), 0, i, a0, b0);
   }
   TT_WAIT_VMCNT(0);  // loads issued past the last tile land before the block exits
 }
@@ -1791,7 +1840,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_q8_kernel(const char* __restrict__ 
     step(nkt - 1, g, std::true_type{});
     ++g;
     __builtin_amdgcn_sched_barrier(0);
-    store_wave_tile_p64<TT_BF16, 0>(acc, tc, tc.i0, tc.j0 + 128 * wave, epi);
+    store_wave_tile_p64<TT_BF16, 0, 32, 4>(acc, tc, tc.i0, tc.j0 + 128 * wave, epi);
     if (++n == ntiles) break;
     tc = tn;
     ra_cur = ra_nxt;
