@@ -1023,7 +1023,6 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
 #pragma unroll
   for (int ni = 0; ni < FN; ++ni) b_mn[ni] = fragmn_base(wn * WT + ni * 32, lane) + P_OPND;
 
-  f32x16 acc[FM][FN];
   uint32_t ao, bo, am[FM], bm[FN];
   // Offsets for k-step s, re-materialised per use (one register each).
   auto refresh = [&](int s) {
@@ -1047,7 +1046,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       fb[i - MV] = Lay::B_K ? read_k(stg, bo + (i - MV) * 4096)
                             : read_mn(stg, bm[i - MV] + s * 8192);
   };
-  auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
+  auto mfma = [&](f32x16 (&acc)[FM][FN], int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
     acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
   };
 
@@ -1065,7 +1064,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   // Issuing a k-tile's 16 loads in one k-step backs up the vector memory
   // path and stalls the MFMAs behind it. The loads are the same in every
   // variant: rows past an expert's end read as zeros without memory traffic.
-  auto step = [&](int kt, int g, auto last_c, auto mv_c) {
+  auto step = [&](f32x16 (&acc)[FM][FN], int kt, int g, auto last_c, auto mv_c) {
     constexpr bool LAST = decltype(last_c)::value;
     constexpr int MV = decltype(mv_c)::value;
     constexpr int NM = MV * FN;       // MFMAs per k-step
@@ -1086,7 +1085,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       refresh(s + 1);
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
-        if (s & 1) mfma(i, a1, b1); else mfma(i, a0, b0);
+        if (s & 1) mfma(acc, i, a1, b1); else mfma(acc, i, a0, b0);
         if (i < NF) {
           if (s & 1) frag(mv_c, cur, s + 1, i, a0, b0); else frag(mv_c, cur, s + 1, i, a1, b1);
         }
@@ -1120,7 +1119,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     refresh(0);
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
-      mfma(i, a1, b1);
+      mfma(acc, i, a1, b1);
       if (!LAST && i < NF) frag(mv_c, nxt, 0, i, a0, b0);
       if constexpr (NM >= 8) {
         if (i % (NM / 8) == (NM / 8 - 1)) issue_one(cur, kr2, to_next2, i / (NM / 8));
@@ -1150,17 +1149,18 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   lds_char* const epi = (lds_char*)epi_raw + wave * P_EPI;
   // One output tile with MV blocks per wave: its k-tiles, then the epilogue
   // (rounds of the wave's blocks that hold rows).
+  // The accumulators are local to a tile (and to its variant), so nothing
+  // carries them from one tile, or variant, to the next.
   auto run_tile = [&](auto mv_c, int& g) {
     constexpr int MV = decltype(mv_c)::value;
+    f32x16 acc[FM][FN];  // blocks mi >= MV are never read
 #pragma unroll
     for (int mi = 0; mi < MV; ++mi)
 #pragma unroll
       for (int ni = 0; ni < FN; ++ni)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
-    for (int kt = 0; kt < nkt_c - 1; ++kt, ++g) step(kt, g, std::false_type{}, mv_c);
-    step(nkt_c - 1, g, std::true_type{}, mv_c);
-    ++g;
+    for (int kt = 0; kt < nkt_c; ++kt, ++g) step(acc, kt, g, std::false_type{}, mv_c);
     __builtin_amdgcn_sched_barrier(0);
     store_wave_tile_p64<ET, WG ? 2 : 0, EPI_ROWS, MV>(acc, tc, tc.i0 + a_row0, tc.j0 + wn * WT,
                                                       epi);
@@ -1196,6 +1196,10 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       rb_nxt = rsrc_b(tn, false);
     }
     ++n;
+    // The last k-step of the finished tile read the next tile's first
+    // fragments. A tile with fewer row blocks than the next tile's variant
+    // did not read the extra A blocks: read every fragment again when the
+    // variants may differ.
     refresh(0);
 #pragma unroll
     for (int i = 0; i < FM + FN; ++i)
