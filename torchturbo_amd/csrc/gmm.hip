@@ -1046,8 +1046,11 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       fb[i - MV] = Lay::B_K ? read_k(stg, bo + (i - MV) * 4096)
                             : read_mn(stg, bm[i - MV] + s * 8192);
   };
-  auto mfma = [&](f32x16 (&acc)[FM][FN], int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
-    acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
+  // fresh: the block's first product of a tile (the accumulator starts at zero)
+  auto mfma = [&](f32x16 (&acc)[FM][FN], int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN],
+                  bool fresh = false) {
+    const f32x16 zero = {};
+    acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], fresh ? zero : acc[i / FN][i % FN]);
   };
 
   lds_char* const lds = (lds_char*)lds_raw;
@@ -1064,8 +1067,9 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   // Issuing a k-tile's 16 loads in one k-step backs up the vector memory
   // path and stalls the MFMAs behind it. The loads are the same in every
   // variant: rows past an expert's end read as zeros without memory traffic.
-  auto step = [&](f32x16 (&acc)[FM][FN], int kt, int g, auto last_c, auto mv_c) {
-    constexpr bool LAST = decltype(last_c)::value;
+  auto step = [&](f32x16 (&acc)[FM][FN], int kt, int g, auto first_c, auto mv_c) {
+    constexpr bool LAST = false;
+    constexpr bool FIRST = decltype(first_c)::value;
     constexpr int MV = decltype(mv_c)::value;
     constexpr int NM = MV * FN;       // MFMAs per k-step
     constexpr int NF = MV + FN;       // fragment reads per k-step
@@ -1085,7 +1089,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       refresh(s + 1);
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
-        if (s & 1) mfma(acc, i, a1, b1); else mfma(acc, i, a0, b0);
+        if (s & 1) mfma(acc, i, a1, b1); else mfma(acc, i, a0, b0, FIRST && s == 0);
         if (i < NF) {
           if (s & 1) frag(mv_c, cur, s + 1, i, a0, b0); else frag(mv_c, cur, s + 1, i, a1, b1);
         }
@@ -1153,14 +1157,10 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   // carries them from one tile, or variant, to the next.
   auto run_tile = [&](auto mv_c, int& g) {
     constexpr int MV = decltype(mv_c)::value;
-    f32x16 acc[FM][FN];  // blocks mi >= MV are never read
-#pragma unroll
-    for (int mi = 0; mi < MV; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < FN; ++ni)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
-    for (int kt = 0; kt < nkt_c; ++kt, ++g) step(acc, kt, g, std::false_type{}, mv_c);
+    f32x16 acc[FM][FN];  // set by the first k-step; blocks mi >= MV are never read
+    step(acc, 0, g, std::true_type{}, mv_c);
+    ++g;
+    for (int kt = 1; kt < nkt_c; ++kt, ++g) step(acc, kt, g, std::false_type{}, mv_c);
     __builtin_amdgcn_sched_barrier(0);
     store_wave_tile_p64<ET, WG ? 2 : 0, EPI_ROWS, MV>(acc, tc, tc.i0 + a_row0, tc.j0 + wn * WT,
                                                       epi);
