@@ -713,16 +713,33 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
   const uint32_t row_bytes = (uint32_t)(t.ldc * 2);
   const int r_l = lane & 31, h = lane >> 5;
   const int rr = lane >> 3, ch = lane & 7;
+  // Per-lane offsets, the same in every round: the eight 8-byte pieces this
+  // lane writes (row r_l, chunk c), the four rows 8 q + rr it reads back
+  // (chunk ch) and where they go in the output.
+  uint32_t wof[8], rof[4], sof[4];
 #pragma unroll
-  for (int mi = 0; mi < NMI; ++mi)
+  for (int c = 0; c < 8; ++c) wof[c] = (uint32_t)(r_l * 128 + ((c ^ ((r_l >> 1) & 7)) << 4) + 8 * h);
 #pragma unroll
-    for (int nh = 0; nh < 2; ++nh) {
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * q + rr;
+    rof[q] = (uint32_t)(r * 128 + ((ch ^ ((r >> 1) & 7)) << 4));
+    sof[q] = (uint32_t)r * row_bytes + (uint32_t)(16 * ch);
+  }
+  const bool col_ok[2] = {cj + 8 * ch < t.J, cj + 64 + 8 * ch < t.J};
+  // Round rd = (mi, nh): the wave's 32 x 64 piece through the region. The
+  // rows read back in round rd are stored after round rd + 1 has been
+  // written, so the LDS read latency hides behind that work (LDS accesses of
+  // one wave complete in order, so the writes never overtake the reads).
+  uint4 back[4];
+#pragma unroll
+  for (int rd = 0; rd <= 2 * NMI; ++rd) {
+    if (rd < 2 * NMI) {
+      const int mi = rd >> 1, nh = rd & 1;
 #pragma unroll
       for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int ni = 2 * nh + nn;
-          const int c = 4 * nn + g;
           // Accumulators are read out of the AGPRs four at a time, where they
           // are converted (a bulk copy would need the whole register file).
           float x0, x1, x2, x3;
@@ -732,23 +749,27 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
                        : "a"(acc[mi][ni][4 * g]), "a"(acc[mi][ni][4 * g + 1]),
                          "a"(acc[mi][ni][4 * g + 2]), "a"(acc[mi][ni][4 * g + 3]));
           const uint2 v = pack4<ET>(x0, x1, x2, x3);
-          *reinterpret_cast<lds_u32x2*>(region + r_l * 128 + ((c ^ ((r_l >> 1) & 7)) << 4) +
-                                        8 * h) =
-              u32x2{v.x, v.y};
-          __builtin_amdgcn_sched_barrier(0);
+          *reinterpret_cast<lds_u32x2*>(region + wof[4 * nn + g]) = u32x2{v.x, v.y};
         }
-      const int64_t col = 64 * nh + 8 * ch;
-      const bool col_ok = cj + col < t.J;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (rd > 0) {
+      const int mi = (rd - 1) >> 1, nh = (rd - 1) & 1;
+      const uint32_t base = (uint32_t)(ROWSTEP * mi) * row_bytes + (uint32_t)(128 * nh);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int r = 8 * q + rr;
-        const uint4 v = read_k(region, (uint32_t)(r * 128 + ((ch ^ ((r >> 1) & 7)) << 4)));
-        const uint32_t off = col_ok ? (uint32_t)(ROWSTEP * mi + r) * row_bytes + (uint32_t)col * 2u
-                                    : DM_OOB;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, (int)off, 0, AUX);
+        const uint32_t off = col_ok[nh] ? sof[q] + base : DM_OOB;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, back[q]), rs, (int)off,
+                                               0, AUX);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (rd < 2 * NMI) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) back[q] = read_k(region, rof[q]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
 }
 
 // Weight-gradient work queues of the persistent kernel. A launch owns one
