@@ -405,15 +405,31 @@ __device__ __forceinline__ void store_wave_tile(const f32x16 (&acc)[4][4], const
         *reinterpret_cast<lds_u32x2*>(region + r * 256 + ((chunk ^ (r & 15)) << 4) + 8 * h) =
             u32x2{v.x, v.y};
       }
+  // Row segments leave through a buffer resource that ends at the expert's
+  // last row (stores past it are dropped; columns past the output width get
+  // an offset past the resource), eight reads ahead of their stores.
+  const int64_t rows = t.I - ri;
+  const int64_t obytes = rows > 0 ? rows * t.ldc * 2 - cj * 2 : 0;
+  const uint32_t nrec = obytes < (int64_t)DM_OOB ? (uint32_t)obytes : DM_OOB;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(t.c + (ri * t.ldc + cj) * 2), (short)0, (int)nrec, 0x00020000);
   const int c = lane & 15;
-  const int64_t gcol = cj + 8 * c;
-  const bool col_ok = gcol < t.J;
+  const bool col_ok = cj + 8 * c < t.J;
+  const uint32_t row_bytes = (uint32_t)(t.ldc * 2);
 #pragma unroll
-  for (int q = 0; q < 32; ++q) {
-    const int r = 4 * q + (lane >> 4);
-    const uint4 v = read_k(region, (uint32_t)(r * 256 + ((c ^ (r & 15)) << 4)));
-    const int64_t grow = ri + r;
-    if (col_ok && grow < t.I) *reinterpret_cast<uint4*>(t.c + (grow * t.ldc + gcol) * 2) = v;
+  for (int q0 = 0; q0 < 32; q0 += 8) {
+    uint4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * (q0 + j) + (lane >> 4);
+      v[j] = read_k(region, (uint32_t)(r * 256 + ((c ^ (r & 15)) << 4)));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * (q0 + j) + (lane >> 4);
+      const uint32_t off = col_ok ? (uint32_t)r * row_bytes + (uint32_t)(16 * c) : DM_OOB;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[j]), rs, (int)off, 0, 0);
+    }
   }
 }
 
@@ -519,13 +535,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
 #pragma unroll
   for (int ni = 0; ni < FN; ++ni) b_mn[ni] = fragmn_base(wn * WT + ni * 32, lane) + DM_TILE;
 
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int mi = 0; mi < FM; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < FN; ++ni)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+  f32x16 acc[FM][FN];  // set by the first k-step (a zero accumulator operand)
 
   // Current fragment offsets, re-materialised once per half step so that the
   // compiler keeps one register per offset instead of one per stage.
@@ -551,8 +561,9 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   };
   // Operands swapped: the accumulator holds C^T blocks, so each lane owns one
   // output row and four consecutive columns per register group.
-  auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN]) {
-    acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], acc[i / FN][i % FN]);
+  auto mfma = [&](int i, const uint4 (&fa)[FM], const uint4 (&fb)[FN], bool fresh = false) {
+    const f32x16 zero = {};
+    acc[i / FN][i % FN] = Mma<ET>::run(fb[i % FN], fa[i / FN], fresh ? zero : acc[i / FN][i % FN]);
   };
 
   lds_char* const s0 = (lds_char*)stage0;
@@ -567,11 +578,11 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   // read and one DMA chunk per slot, in this order (sched_barrier pins it).
   // Loads past the last tile fall outside the resource (zeros) and land in
   // stages that are never read again.
-  auto step = [&](int kt, lds_char* cur, lds_char* nxt, lds_char* refill) {
+  auto step = [&](int kt, lds_char* cur, lds_char* nxt, lds_char* refill, auto first_c) {
     refresh();
 #pragma unroll
     for (int i = 0; i < FM * FN; ++i) {
-      mfma(i, a0, b0);
+      mfma(i, a0, b0, decltype(first_c)::value);
       if (i < FM + FN) frag(cur, 1, i, a1, b1);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -595,11 +606,18 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   refresh();
 #pragma unroll
   for (int i = 0; i < FM + FN; ++i) frag(s0, 0, i, a0, b0);
-  for (int kt = 0; kt < nkt; kt += DM_ST) {
-    step(kt, s0, s1, s3);
-    if (kt + 1 < nkt) step(kt + 1, s1, s2, s0);
-    if (kt + 2 < nkt) step(kt + 2, s2, s3, s1);
-    if (kt + 3 < nkt) step(kt + 3, s3, s0, s2);
+  // The first k-tile starts the accumulators (a zero operand in its first
+  // k-step); the loop continues with the same stage rotation.
+  const std::false_type more{};
+  step(0, s0, s1, s3, std::true_type{});
+  if (1 < nkt) step(1, s1, s2, s0, more);
+  if (2 < nkt) step(2, s2, s3, s1, more);
+  if (3 < nkt) step(3, s3, s0, s2, more);
+  for (int kt = DM_ST; kt < nkt; kt += DM_ST) {
+    step(kt, s0, s1, s3, more);
+    if (kt + 1 < nkt) step(kt + 1, s1, s2, s0, more);
+    if (kt + 2 < nkt) step(kt + 2, s2, s3, s1, more);
+    if (kt + 3 < nkt) step(kt + 3, s3, s0, s2, more);
   }
   TT_WAIT_VMCNT(0);  // every DMA has landed before the stages are reused
   __syncthreads();   // every wave is past its last fragment read
