@@ -238,6 +238,13 @@ int tt_gated_act_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, int ac
  * TorchGroupedMatmul (ops/providers/native/grouped_matmul.py:16-56) and
  * grouped_gemm.ops.gmm (ops/providers/cuda/grouped_matmul.py:34-36).
  * dtype bf16/f16 (MFMA, fp32 accumulation) or f32.
+ * Concurrency: weight-gradient launches that take the persistent kernel
+ * (at most 512 rows per expert on average, M <= 512 * E) keep their work
+ * queue in one of 64 slots of a per-process device array, taken in turn by
+ * successive launches (each launch clears its slot on its stream first). At
+ * most 64 such launches may be in flight at once across all streams of a
+ * device; launches on one stream never overlap, so a single stream has no
+ * limit.
  * fwd:   y[M, N] = x[M, K] @ W[e] with W [E, K, N]; trans_b: W [E, N, K], W[e]^T. */
 int tt_gmm_fwd(const void* x, const void* w, int dtype, int64_t m, int64_t k, int64_t n,
                int32_t num_experts, int32_t trans_b, const int64_t* counts, void* y,
