@@ -35,6 +35,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source flags. gmm.hip: no cross-lane merging of atomics (the merge
+# waits for the atomic's return right away, stalling the GEMM pipeline on its
+# in-flight loads; the queue atomics there are issued by one lane anyway).
+SOURCE_FLAGS = {
+    "gmm.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -61,7 +69,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = build_dir / (src.stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
+        cmd = [cc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-I", str(PKG.parent / "include"),
+               "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -644,10 +644,18 @@ __device__ __forceinline__ void tile_at(int L, const char* p0, const char* p1, c
                                         const int64_t* row_start, const int* tile_start,
                                         TileDesc& t) {
   const int slot = L / tiles_j, jt = L % tiles_j;
-  int lo = 0, hi = E - 1;  // last e with tile_start[e] <= slot
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (tile_start[mid] <= slot) lo = mid; else hi = mid - 1;
+  // Last e with tile_start[e] <= slot (tile_start is non-decreasing and
+  // tile_start[0] = 0): the wave's 64 lanes test 64 evenly spaced candidates
+  // of the range at once, and the count of lanes that pass narrows the range
+  // to one stride (one LDS round trip per 64-fold narrowing).
+  const int lane = __lane_id();
+  int lo = 0, span = E;
+  while (span > 1) {
+    const int stride = (span + 63) >> 6;
+    const bool ok = lane * stride < span && tile_start[lo + lane * stride] <= slot;
+    const int c = __popcll(__ballot(ok)) - 1;
+    lo += c * stride;
+    span = min(stride, span - c * stride);
   }
   // Schedule values are uniform: keep them (and all that derives from them)
   // in scalar registers.
