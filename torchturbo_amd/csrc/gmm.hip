@@ -40,7 +40,9 @@
 //   bytes and each wave decodes its own rows in hardware, multiplies by the
 //   block scale and rounds to bf16 (exactly bf16(f32(q) * f32(scale))) into
 //   one of three rotating bf16 tiles, overlapped with the previous k-tile's
-//   MFMAs. An fp32 fallback kernel serves fp32 operands.
+//   MFMAs.
+// * gmm_f32_kernel (fp32 operands): 64x64 tiles on fp32 MFMAs
+//   (v_mfma_f32_32x32x2_f32).
 //
 // Tile schedule: fwd/dgrad blocks walk (expert, m-tile, n-tile) slots whose
 // count is only known on the device; every block derives its slot from the
@@ -1910,6 +1912,12 @@ __global__ __launch_bounds__(DM_NT) void gmm_q8_kernel(const char* __restrict__ 
   TT_WAIT_VMCNT(0);  // loads issued past the last tile land before the block exits
 }
 
+// fp32 operands (the toy configuration, fp32 LoRA adapters): 64x64 output
+// tiles, each wave one 32x32 block on v_mfma_f32_32x32x2_f32 (full fp32
+// products and sums, fp32 accumulation). A 16-deep k-tile is staged in LDS as
+// [k][row] and [k][col]; MFMA step s takes k = s (lanes 0-31) and k = s + 8
+// (lanes 32-63). B goes in as the first operand, so each lane ends with one
+// output row and four consecutive columns per group (16-byte stores).
 template <int MODE, bool TRANS_B>
 __global__ __launch_bounds__(256) void gmm_f32_kernel(const float* __restrict__ p0,
                                                       const float* __restrict__ p1,
@@ -1935,8 +1943,10 @@ __global__ __launch_bounds__(256) void gmm_f32_kernel(const float* __restrict__ 
   float* Cp = reinterpret_cast<float*>(t.c);
   const int64_t I = t.I, J = t.J, R = t.R, lda = t.lda, ldb = t.ldb;
   const int64_t i0 = t.i0, j0 = t.j0;
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  float acc[4][4] = {};
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;  // the wave's 32x32 block
+  const int l32 = lane & 31, h = lane >> 5;
+  f32x16 acc = {};
   for (int64_t k0 = 0; k0 < R; k0 += BKF) {
     for (int q = threadIdx.x; q < BKF * BT; q += 256) {
       const int kk = q / BT, rr = q % BT;
@@ -1946,27 +1956,26 @@ __global__ __launch_bounds__(256) void gmm_f32_kernel(const float* __restrict__ 
     }
     __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < BKF; ++kk) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        av[u] = sa[kk][ty * 4 + u];
-        bv[u] = sb[kk][tx * 4 + u];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[u][v] += av[u] * bv[v];
-    }
+    for (int s = 0; s < BKF / 2; ++s)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(sb[s + 8 * h][wc + l32], sa[s + 8 * h][wr + l32],
+                                                 acc, 0, 0, 0);
     __syncthreads();
   }
+  const int64_t gi = i0 + wr + l32;
+  if (gi >= I) return;
+  float* row = Cp + gi * t.ldc;
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int g = 0; g < 4; ++g) {
+    const int64_t gj = j0 + wc + 8 * g + 4 * h;
+    if (gj + 3 < J && ((t.ldc | gj) & 3) == 0) {
+      *reinterpret_cast<float4*>(row + gj) = float4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2],
+                                                    acc[4 * g + 3]};
+    } else {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t gi = i0 + ty * 4 + u, gj = j0 + tx * 4 + v;
-      if (gi < I && gj < J) Cp[gi * t.ldc + gj] = acc[u][v];
+      for (int v = 0; v < 4; ++v)
+        if (gj + v < J) row[gj + v] = acc[4 * g + v];
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
