@@ -867,6 +867,36 @@ def test_grouped_matmul_many_tiles(hip_ops, dtype, trans_b, E, M, K, N):
         assert torch.count_nonzero(w.grad[e]) == 0
 
 
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_grouped_matmul_long_wgrad_integer_exact(hip_ops, trans_b):
+    """Weight gradients with long expert reductions (mean load above 512 rows: the
+    four-stage kernel, one output tile per block) on small-integer operands, so every
+    sum is exact in fp32 and dW is the exact product rounded once. Zipf loads with
+    empty experts, a one-row expert and experts shorter than three 32-deep k-tiles;
+    16 output tiles per expert."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    E, K, N = 64, 1024, 768
+    counts = _zipf_counts(E, E * 1024, seed=5, empty=(3, 17, 40))
+    counts[11], counts[12] = 1, 70  # below three k-tiles
+    counts[int(counts.argmax())] -= 71
+    M = int(counts.sum())
+    g = torch.Generator(device=DEV).manual_seed(3)
+    x = torch.randint(-3, 4, (M, K), generator=g, device=DEV).to(torch.bfloat16)
+    wshape = (E, N, K) if trans_b else (E, K, N)
+    w = torch.randint(-3, 4, wshape, generator=g, device=DEV).to(torch.bfloat16).requires_grad_()
+    dy = torch.randint(-3, 4, (M, N), generator=g, device=DEV).to(torch.bfloat16)
+    for _ in range(2):  # twice: nothing carries over between launches
+        w.grad = None
+        y = hip_ops.grouped_matmul(x, w, counts.to(DEV), trans_b=trans_b)
+        y.backward(dy)
+        xs = torch.split(x.float(), counts.tolist())
+        ds = torch.split(dy.float(), counts.tolist())
+        for e in range(E):
+            dwe = xs[e].t() @ ds[e]  # [K, N], exact (integer sums below 2^24)
+            ref = (dwe.t() if trans_b else dwe).to(torch.bfloat16)
+            assert torch.equal(w.grad[e], ref), (e, int(counts[e]))
+
+
 # ---------------------------------------------------------------------------
 # FP8 block-scaled grouped GEMM
 # ---------------------------------------------------------------------------
