@@ -49,8 +49,9 @@
 // per-expert counts (a block-wide scan in LDS) and blocks past the last slot
 // exit. fwd/dgrad block ids are remapped so that consecutive slots (sharing an
 // A panel and an expert's weights) run on one XCD and its L2. wgrad blocks
-// take experts longest-first and are left in hardware round-robin order, so
-// the tiles of a heavily loaded expert spread over all XCDs.
+// take experts longest-first; each expert's tiles go to one pair of XCDs
+// (one-tile-per-block kernel) or to every XCD as rectangles (persistent
+// kernel), so that the XCDs share its activation panels in L2.
 #include "common.h"
 
 #include <atomic>
@@ -164,6 +165,20 @@ struct TileDesc {
   int e;
 };
 
+// Weight-gradient tiles of one block per tile (gmm_mfma_kernel): each
+// expert's output tiles go to one pair of XCDs, half of its tile grid to
+// each, so an XCD's blocks re-read an expert's activation panels from L2
+// instead of all eight XCDs reading them from memory (per expert, half the
+// panels that the eight-XCD rectangles read: Qwen fc1 20 instead of 40, fc2
+// 14 instead of 32; 14 and 11 are the minimum). Returns how the grid splits:
+// 1 along its rows (tile rows i), 2 along its columns, 0 when neither count
+// is even (then every XCD takes a rectangle of every expert).
+__host__ __device__ inline int wgrad_pair_split(int tiles_i, int tiles_j) {
+  const bool ei = tiles_i % 2 == 0, ej = tiles_j % 2 == 0;
+  if (ei && (!ej || tiles_i / 2 + tiles_j <= tiles_i + tiles_j / 2)) return 1;
+  return ej ? 2 : 0;
+}
+
 template <int NT, int BM, int BN, int MODE, bool TRANS_B, int ESZ, int WSZ>
 __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t K, int64_t N,
                               int E, const int64_t* __restrict__ counts, int tiles_i, int tiles_j,
@@ -176,15 +191,29 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
     __shared__ int lpt_expert;
     const int lb = blockIdx.x;
     const int per = tiles_i * tiles_j;
-    const int rank = lb / per;
+    int rank = lb / per;
     const int rem = lb % per;
-    // Block b runs on XCD b % 8. When an expert's tile grid splits into 8
-    // equal rectangles (a x c of them), XCD x takes rectangle x: its blocks
-    // then share a few activation panels in that XCD's L2 (a rectangle of
-    // h x w tiles reads h + w panels), while a heavily loaded expert still
-    // spreads over all XCDs. Otherwise tiles go in row order.
+    const int split = wgrad_pair_split(tiles_i, tiles_j);
+    // Block b runs on XCD b % 8. XCD pair p = (b % 8) / 2 takes the experts of
+    // ranks 8m + p and 8m + 7 - p (longest first, a snake over the four
+    // pairs, so the pairs' loads even out), and XCD 2p + h the half h of each
+    // one's tile grid, in row order: the pair's blocks of one expert run
+    // together and share its panels in their XCD's L2. The grid holds
+    // 8 ceil(E / 8) x per blocks; ranks past the last expert exit.
     int h = 0, w = 0, c = 0;
-    if (per % 8 == 0) {
+    if (split != 0) {
+      const int x = lb % 8, j = lb / 8, pr = x >> 1, hf = x & 1;
+      const int half = per / 2;
+      const int k = j / half, t = j % half;
+      rank = 8 * (k >> 1) + ((k & 1) ? 7 - pr : pr);
+      if (split == 1) {
+        it = hf * (tiles_i / 2) + t / tiles_j;
+        jt = t % tiles_j;
+      } else {
+        it = t / (tiles_j / 2);
+        jt = hf * (tiles_j / 2) + t % (tiles_j / 2);
+      }
+    } else if (per % 8 == 0) {
       int best = 1 << 30;
       for (int a = 1; a <= 8; a <<= 1) {
         const int cc = 8 / a;
@@ -193,7 +222,9 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
         if (hh + ww < best) { best = hh + ww; h = hh; w = ww; c = cc; }
       }
     }
-    if (h > 0) {
+    if (split != 0) {
+      // (it, jt) set above
+    } else if (h > 0) {
       const int x = rem % 8, j = rem / 8;
       it = (x / c) * h + j / w;
       jt = (x % c) * w + j % w;
@@ -2029,6 +2060,10 @@ int allow_lds(F* kernel, size_t lds, size_t& allowed) {
 template <int MODE, bool TB, int ET, bool KMASK>
 int launch_mfma_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
                   int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj) {
+  // Weight gradients on XCD pairs: eight blocks per group of eight expert
+  // ranks and tile (see describe_tile).
+  if (MODE == MODE_WGRAD && wgrad_pair_split(ti, tj) != 0)
+    nblk = 8 * (int64_t)((E + 7) / 8) * ti * tj;
   const size_t lds = schedule_bytes(E);  // the stages are static LDS
   static size_t allowed = 64 * 1024;
   const int rc = allow_lds(&gmm_mfma_kernel<MODE, TB, ET, KMASK>, lds, allowed);
