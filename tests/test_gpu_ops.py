@@ -803,6 +803,35 @@ def test_grouped_matmul_integer_exact(hip_ops):
     assert torch.equal(wd.grad.cpu(), wr.grad.to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("E,rows", [(5, 150), (5, 1100), (13, 900), (16, 40)])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_grouped_matmul_wgrad_writes_every_tile(dtype, E, rows, trans_b):
+    """tt_gmm_wgrad into a NaN-filled output: every expert's whole gradient is written
+    (empty experts get zeros), whatever the kernel (fp32, persistent short-reduction,
+    one tile per block on XCD pairs) and whether E is a multiple of 8."""
+    from torchturbo_amd import _lib
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    g = torch.Generator().manual_seed(E * 1000 + rows)
+    counts = torch.randint(0, 2 * rows, (E,), generator=g)
+    counts[1] = 0
+    M, K, N = int(counts.sum()), 512, 768
+    x = torch.randint(-2, 3, (M, K), generator=g).to(dtype).to(DEV)
+    dy = torch.randint(-2, 3, (M, N), generator=g).to(dtype).to(DEV)
+    dw = torch.full((E, N, K) if trans_b else (E, K, N), float("nan"), dtype=dtype, device=DEV)
+    cnt = counts.to(DEV)
+    _lib.call("tt_gmm_wgrad", _lib.ptr(x), _lib.ptr(dy), _lib.dtype_code(dtype), M, K, N, E,
+              int(trans_b), _lib.ptr(cnt), _lib.ptr(dw), _lib.stream())
+    torch.cuda.synchronize()
+    xs = torch.split(x.float(), counts.tolist())
+    ds = torch.split(dy.float(), counts.tolist())
+    for e in range(E):
+        ref = xs[e].t() @ ds[e]  # [K, N]; integer sums, exact in fp32
+        ref = (ref.t() if trans_b else ref).to(dtype)
+        assert torch.equal(dw[e], ref), (e, int(counts[e]))
+
+
 def _zipf_counts(E, M, seed, empty=(3, 17)):
     """Zipf(1.1)-skewed expert loads summing to M, with some empty experts."""
     g = torch.Generator().manual_seed(seed)
@@ -868,15 +897,17 @@ def test_grouped_matmul_many_tiles(hip_ops, dtype, trans_b, E, M, K, N):
 
 
 @pytest.mark.parametrize("trans_b", [False, True])
-def test_grouped_matmul_long_wgrad_integer_exact(hip_ops, trans_b):
+@pytest.mark.parametrize("E,K,N", [(64, 1024, 768), (13, 1024, 768), (13, 768, 768)])
+def test_grouped_matmul_long_wgrad_integer_exact(hip_ops, trans_b, E, K, N):
     """Weight gradients with long expert reductions (mean load above 512 rows: the
     four-stage kernel, one output tile per block) on small-integer operands, so every
     sum is exact in fp32 and dW is the exact product rounded once. Zipf loads with
-    empty experts, a one-row expert and experts shorter than three 32-deep k-tiles;
-    16 output tiles per expert."""
+    empty experts, a one-row expert and experts shorter than three 32-deep k-tiles.
+    With a 4 x 3 tile grid every expert's tiles go to one pair of XCDs (at E = 13, not a
+    multiple of 8, the blocks of ranks past the last expert exit); a 3 x 3 grid (no even
+    side) takes the all-XCD mapping."""
     torch.backends.cuda.matmul.allow_tf32 = False
-    E, K, N = 64, 1024, 768
-    counts = _zipf_counts(E, E * 1024, seed=5, empty=(3, 17, 40))
+    counts = _zipf_counts(E, E * 1024, seed=5, empty=(3, 7) if E < 20 else (3, 17, 40))
     counts[11], counts[12] = 1, 70  # below three k-tiles
     counts[int(counts.argmax())] -= 71
     M = int(counts.sum())

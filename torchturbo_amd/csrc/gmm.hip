@@ -179,7 +179,9 @@ __host__ __device__ inline int wgrad_pair_split(int tiles_i, int tiles_j) {
   return ej ? 2 : 0;
 }
 
-template <int NT, int BM, int BN, int MODE, bool TRANS_B, int ESZ, int WSZ>
+// PAIRS: weight-gradient tiles on XCD pairs (wgrad_pair_split); the launch
+// must then size the grid as 8 ceil(E / 8) x tiles_i x tiles_j.
+template <int NT, int BM, int BN, int MODE, bool TRANS_B, int ESZ, int WSZ, bool PAIRS = false>
 __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t K, int64_t N,
                               int E, const int64_t* __restrict__ counts, int tiles_i, int tiles_j,
                               int64_t* row_start, int* tile_start, TileDesc& t) {
@@ -193,7 +195,7 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
     const int per = tiles_i * tiles_j;
     int rank = lb / per;
     const int rem = lb % per;
-    const int split = wgrad_pair_split(tiles_i, tiles_j);
+    const int split = PAIRS ? wgrad_pair_split(tiles_i, tiles_j) : 0;
     // Block b runs on XCD b % 8. XCD pair p = (b % 8) / 2 takes the experts of
     // ranks 8m + p and 8m + 7 - p (longest first, a snake over the four
     // pairs, so the pairs' loads even out), and XCD 2p + h the half h of each
@@ -496,7 +498,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   int* tile_start = reinterpret_cast<int*>(row_start + E + 1);
 
   TileDesc t;
-  if (!describe_tile<DM_NT, DM_BM, DM_BN, MODE, TRANS_B, 2, 2>(p0, p1, out, K, N, E, counts,
+  if (!describe_tile<DM_NT, DM_BM, DM_BN, MODE, TRANS_B, 2, 2, true>(p0, p1, out, K, N, E, counts,
                                                                  tiles_i, tiles_j, row_start,
                                                                  tile_start, t))
     return;
