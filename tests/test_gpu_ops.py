@@ -832,6 +832,80 @@ def test_grouped_matmul_wgrad_writes_every_tile(dtype, E, rows, trans_b):
         assert torch.equal(dw[e], ref), (e, int(counts[e]))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("E", [5, 13])
+@pytest.mark.parametrize("K,N", [(512, 768), (64, 64)])
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_grouped_matmul_fwd_dgrad_write_every_row(dtype, E, K, N, trans_b):
+    """tt_gmm_fwd / tt_gmm_dgrad into NaN-filled outputs with small-integer operands:
+    every row of every expert is written, exactly (64-deep persistent kernel for
+    reductions above 64, the one-tile kernel for 64, fp32; partial and empty experts)."""
+    from torchturbo_amd import _lib
+
+    g = torch.Generator().manual_seed(E * 7 + K)
+    counts = torch.randint(0, 700, (E,), generator=g)
+    counts[2] = 0
+    counts[3] = 1
+    M = int(counts.sum())
+    x = torch.randint(-2, 3, (M, K), generator=g).to(dtype).to(DEV)
+    dy = torch.randint(-2, 3, (M, N), generator=g).to(dtype).to(DEV)
+    wshape = (E, N, K) if trans_b else (E, K, N)
+    w = torch.randint(-2, 3, wshape, generator=g).to(dtype).to(DEV)
+    y = torch.full((M, N), float("nan"), dtype=dtype, device=DEV)
+    dx = torch.full((M, K), float("nan"), dtype=dtype, device=DEV)
+    cnt = counts.to(DEV)
+    args = (_lib.dtype_code(dtype), M, K, N, E, int(trans_b), _lib.ptr(cnt))
+    _lib.call("tt_gmm_fwd", _lib.ptr(x), _lib.ptr(w), *args, _lib.ptr(y), _lib.stream())
+    _lib.call("tt_gmm_dgrad", _lib.ptr(dy), _lib.ptr(w), *args, _lib.ptr(dx), _lib.stream())
+    torch.cuda.synchronize()
+    wf = w.float()
+    yr, dxr, s0 = torch.empty(M, N, device=DEV), torch.empty(M, K, device=DEV), 0
+    for e, c in enumerate(counts.tolist()):
+        we = wf[e].t() if trans_b else wf[e]  # [K, N]
+        yr[s0:s0 + c] = x[s0:s0 + c].float() @ we
+        dxr[s0:s0 + c] = dy[s0:s0 + c].float() @ we.t()
+        s0 += c
+    assert torch.equal(y, yr.to(dtype))
+    assert torch.equal(dx, dxr.to(dtype))
+
+
+@pytest.mark.parametrize("E", [5, 13])
+@pytest.mark.parametrize("K,N", [(512, 768), (64, 64)])
+def test_grouped_matmul_fp8_write_every_row(E, K, N):
+    """tt_gmm_fp8_fwd / _dgrad into NaN-filled outputs: e4m3 weights holding small
+    integers with unit block scales, so every output is an exact integer sum (the
+    persistent 128x512 kernel for reductions above 64, the 256x256 kernel for 64)."""
+    from torchturbo_amd import _lib
+
+    g = torch.Generator().manual_seed(E * 11 + K)
+    counts = torch.randint(0, 700, (E,), generator=g)
+    counts[2] = 0
+    counts[3] = 1
+    M = int(counts.sum())
+    x = torch.randint(-2, 3, (M, K), generator=g).to(torch.bfloat16).to(DEV)
+    dy = torch.randint(-2, 3, (M, N), generator=g).to(torch.bfloat16).to(DEV)
+    wq = torch.randint(-2, 3, (E, N, K), generator=g).float()
+    q = wq.to(torch.float8_e4m3fn).to(DEV)
+    sc = torch.ones(E, (N + 127) // 128, (K + 127) // 128, dtype=torch.bfloat16, device=DEV)
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+    dx = torch.full((M, K), float("nan"), dtype=torch.bfloat16, device=DEV)
+    cnt = counts.to(DEV)
+    bf = _lib.dtype_code(torch.bfloat16)
+    _lib.call("tt_gmm_fp8_fwd", _lib.ptr(x), _lib.ptr(q), _lib.ptr(sc), bf, M, K, N, E,
+              _lib.ptr(cnt), _lib.ptr(y), _lib.stream())
+    _lib.call("tt_gmm_fp8_dgrad", _lib.ptr(dy), _lib.ptr(q), _lib.ptr(sc), bf, M, K, N, E,
+              _lib.ptr(cnt), _lib.ptr(dx), _lib.stream())
+    torch.cuda.synchronize()
+    wd = wq.to(DEV)
+    yr, dxr, s0 = torch.empty(M, N, device=DEV), torch.empty(M, K, device=DEV), 0
+    for e, c in enumerate(counts.tolist()):
+        yr[s0:s0 + c] = x[s0:s0 + c].float() @ wd[e].t()
+        dxr[s0:s0 + c] = dy[s0:s0 + c].float() @ wd[e]
+        s0 += c
+    assert torch.equal(y, yr.to(torch.bfloat16))
+    assert torch.equal(dx, dxr.to(torch.bfloat16))
+
+
 def _zipf_counts(E, M, seed, empty=(3, 17)):
     """Zipf(1.1)-skewed expert loads summing to M, with some empty experts."""
     g = torch.Generator().manual_seed(seed)
