@@ -259,6 +259,24 @@ int tt_gmm_wgrad(const void* x, const void* dy, int dtype, int64_t m, int64_t k,
                  int32_t num_experts, int32_t trans_b, const int64_t* counts, void* dw,
                  void* stream);
 
+/* fwd / dgrad with the activation rows gathered: packed row r is row
+ * src_of_row[r] of x_src / dy_src ([src_rows, R], R = k for fwd, n for dgrad;
+ * src_of_row: device int32 [m], e.g. token_of_row of tt_route_index). One
+ * launch replaces a permutation followed by the GEMM (the index_select of
+ * ops/providers/native/moe_permutation.py:43 feeding
+ * ops/providers/native/grouped_matmul.py:16-56), with no packed copy of the
+ * activations; the result equals tt_gmm_fwd / tt_gmm_dgrad on the gathered
+ * rows bit for bit. bf16 / f16, R a multiple of 64 above 64, sources under
+ * 2 GiB; other problems return TT_ERR_INVALID. */
+int tt_gmm_fwd_gather(const void* x_src, int64_t src_rows, const int32_t* src_of_row,
+                      const void* w, int dtype, int64_t m, int64_t k, int64_t n,
+                      int32_t num_experts, int32_t trans_b, const int64_t* counts, void* y,
+                      void* stream);
+int tt_gmm_dgrad_gather(const void* dy_src, int64_t src_rows, const int32_t* src_of_row,
+                        const void* w, int dtype, int64_t m, int64_t k, int64_t n,
+                        int32_t num_experts, int32_t trans_b, const int64_t* counts, void* dx,
+                        void* stream);
+
 /* FP8 e4m3 weights with 128x128 block scales, HF [out, in] orientation:
  * qw [E, N, K] bytes, scale [E, ceil(N/128), ceil(K/128)] (bf16 or f32).
  * Weight element = bf16(f32(q) * f32(scale)), the rule of the reference's

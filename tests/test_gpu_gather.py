@@ -1,0 +1,85 @@
+"""Grouped GEMMs that gather their activation rows (GPU).
+
+``tt_gmm_fwd_gather`` / ``tt_gmm_dgrad_gather`` read packed row r from row
+``src_of_row[r]`` of an unpacked source, so a permutation and the GEMM after it
+are one launch. They must equal the packed GEMMs (``tt_gmm_fwd`` /
+``tt_gmm_dgrad``) on ``src[src_of_row]`` bit for bit: same operand values, same
+reduction order. Cases: many tiles per persistent block (Qwen shapes), Zipf
+loads with empty and one-row experts, duplicated and unused source rows, both
+weight layouts, bf16 and f16.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _loads(E, M, seed):
+    g = torch.Generator().manual_seed(seed)
+    rank = torch.randperm(E, generator=g).double() + 1.0
+    c = (rank.pow(-1.1) / rank.pow(-1.1).sum() * M).floor().long()
+    c[min(3, E - 1)] = 0
+    c[min(4, E - 1)] = 1
+    c[int(rank.argmin())] += M - int(c.sum())
+    assert int(c.sum()) == M and int(c.min()) >= 0
+    return c
+
+
+# dtype, trans_b, E, M (packed rows), T (source rows), K, N
+CASES = [
+    (torch.bfloat16, False, 128, 65536, 8192, 2048, 1536),
+    (torch.bfloat16, True, 64, 32768, 4096, 768, 2048),
+    (torch.float16, False, 13, 9000, 2000, 512, 768),
+    (torch.bfloat16, False, 5, 700, 60, 128, 192),
+]
+
+
+@pytest.mark.parametrize("dtype,trans_b,E,M,T,K,N", CASES,
+                         ids=lambda v: str(v).replace("torch.", ""))
+def test_gathered_rows_equal_the_packed_gemm(dtype, trans_b, E, M, T, K, N):
+    from torchturbo_amd import _lib
+
+    counts = _loads(E, M, seed=E + K)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    xs = torch.randn(T, K, generator=g, device=DEV).to(dtype)
+    dys = torch.randn(T, N, generator=g, device=DEV).to(dtype)
+    rows = torch.randint(0, T, (M,), generator=g, device=DEV, dtype=torch.int32)
+    wshape = (E, N, K) if trans_b else (E, K, N)
+    w = (torch.randn(*wshape, generator=g, device=DEV) * 0.05).to(dtype)
+    cnt = counts.to(DEV)
+    args = (_lib.dtype_code(dtype), M, K, N, E, int(trans_b), _lib.ptr(cnt))
+    st = _lib.stream()
+    y_p = torch.empty(M, N, dtype=dtype, device=DEV)
+    dx_p = torch.empty(M, K, dtype=dtype, device=DEV)
+    x_packed, dy_packed = xs[rows.long()], dys[rows.long()]
+    _lib.call("tt_gmm_fwd", _lib.ptr(x_packed), _lib.ptr(w), *args, _lib.ptr(y_p), st)
+    _lib.call("tt_gmm_dgrad", _lib.ptr(dy_packed), _lib.ptr(w), *args, _lib.ptr(dx_p), st)
+    for _ in range(2):  # twice into NaN-filled outputs: every row written, nothing carried over
+        y_g = torch.full((M, N), float("nan"), dtype=dtype, device=DEV)
+        dx_g = torch.full((M, K), float("nan"), dtype=dtype, device=DEV)
+        _lib.call("tt_gmm_fwd_gather", _lib.ptr(xs), T, _lib.ptr(rows), _lib.ptr(w), *args,
+                  _lib.ptr(y_g), st)
+        _lib.call("tt_gmm_dgrad_gather", _lib.ptr(dys), T, _lib.ptr(rows), _lib.ptr(w), *args,
+                  _lib.ptr(dx_g), st)
+        torch.cuda.synchronize()
+        assert torch.equal(y_g, y_p)
+        assert torch.equal(dx_g, dx_p)
+
+
+def test_gather_rejects_reductions_it_does_not_cover():
+    """Reductions of 64 or fewer, or not a multiple of 64, take kernels without a
+    gathered path: the call fails before any launch."""
+    from torchturbo_amd import _lib
+
+    counts = torch.tensor([3, 5], device=DEV)
+    xs = torch.zeros(8, 96, dtype=torch.bfloat16, device=DEV)
+    rows = torch.zeros(8, dtype=torch.int32, device=DEV)
+    w = torch.zeros(2, 96, 64, dtype=torch.bfloat16, device=DEV)
+    y = torch.empty(8, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        _lib.call("tt_gmm_fwd_gather", _lib.ptr(xs), 8, _lib.ptr(rows), _lib.ptr(w), 1, 8, 96, 64,
+                  2, 0, _lib.ptr(counts), _lib.ptr(y), _lib.stream())

@@ -57,6 +57,9 @@ def test_library_exports_every_declared_symbol(lib):
     ("tt_gmm_fwd", (None, None, 5, 16, 16, 16, 2, 0, None, None, None), "dtype"),
     ("tt_gmm_fwd", (None, None, 1, 16, 16, 16, 0, 0, None, None, None), "num_experts"),
     ("tt_gmm_fp8_fwd", (None, None, None, 2, 16, 16, 16, 2, None, None, None), "scales"),
+    ("tt_gmm_fwd_gather", (None, 8, None, None, 1, 16, 128, 16, 2, 0, None, None, None),
+     "row map"),
+    ("tt_gmm_fwd_gather", (None, 8, None, None, 0, 16, 128, 16, 2, 0, None, None, None), "dtype"),
     ("tt_route_index", (None, 4, 2, 8, None, 0, None, None, None, None, None, 0, None),
      "workspace"),
     ("tt_sort_chunks", (None, 0, 4, 4, None, None, 5000, None, 0, None, None, None), "4096"),

@@ -321,6 +321,10 @@ constexpr int DM_BM = 256, DM_BN = 256, DM_BK = 32, DM_ST = 4, DM_NT = 256;
 constexpr int DM_TILE = DM_BM * DM_BK * 2;  // bytes of one operand tile (16 KiB)
 constexpr int DM_STAGE = 2 * DM_TILE;       // A tile then B tile
 constexpr uint32_t DM_OOB = 0xFFFFFFF0u;    // buffer offset past any resource
+// Gathered A rows: the offset of a row past an expert's end, past any gathered
+// source (sources are smaller than 2 GiB) with room for the chunk and k-tile
+// offsets added to it.
+constexpr uint32_t GA_NOROW = 0x80000000u;
 
 typedef __attribute__((ext_vector_type(4))) int i32x4;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
@@ -937,15 +941,20 @@ __device__ __forceinline__ int wgrad_tile_at(int q, int cls, int nx, int cx, con
   return nkt > 2 ? nkt : 2;
 }
 
-template <int MODE, bool TRANS_B, int ET, bool KMASK>
+// GA (fwd / dgrad): the A rows are gathered, row r of the packed order being
+// row arow[r] of p0 ([asrc_rows, lda]); see gather_rows below.
+template <int MODE, bool TRANS_B, int ET, bool KMASK, bool GA = false>
 __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__ p0,
                                                         const char* __restrict__ p1,
                                                         char* __restrict__ out, int64_t M,
                                                         int64_t K, int64_t N, int E,
                                                         const int64_t* __restrict__ counts,
-                                                        int tiles_i, int tiles_j, int qslot) {
+                                                        int tiles_i, int tiles_j, int qslot,
+                                                        const int32_t* __restrict__ arow,
+                                                        int64_t asrc_rows) {
   constexpr bool WG = MODE == MODE_WGRAD;
   static_assert(!(WG && KMASK), "wgrad reduces over rows (no K-major tail)");
+  static_assert(!(GA && (WG || KMASK)), "gathered A rows: fwd / dgrad without a K-major tail");
   typedef Layout<MODE, TRANS_B> Lay;
   constexpr int WT = 128, FM = 4, FN = 4;
   __shared__ __align__(16) char lds_raw[2 * P_STAGE];
@@ -1036,6 +1045,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   // MN-major over the expert's rows, so reduction rows past the expert's
   // end read as zeros.
   auto rsrc_a = [&](const TileDesc& t, bool valid) -> i32x4 {
+    if constexpr (GA) return make_rsrc(p0, asrc_rows * lda * 2);  // the whole source
     if (!valid) return make_rsrc(p0, 0);
     if constexpr (WG) return make_rsrc(t.a + t.i0 * 2, t.R * t.lda * 2 - t.i0 * 2);
     const int64_t toff = t.i0 * t.lda * 2;
@@ -1066,6 +1076,38 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       tile_at<MODE, TRANS_B, 2>(pos + G, p0, p1, out, K, N, E, tiles_j, row_start, tile_start,
                                 tn);
   }
+  // GA: the source row of each of the lane's eight A rows of a tile (K-major
+  // rows 64 wave + lane / 8 + 8 q), loaded when the tile is decoded; rows past
+  // the expert's end get GA_NOROW. gather_offsets turns them into byte offsets
+  // after a wait that the k-loop makes anyway (the first k-tile's), so the
+  // index loads never stall the loop.
+  uint32_t ro_cur[8], ro_nxt[8];
+  auto gather_rows = [&](const TileDesc& t, bool valid, uint32_t (&ro)[8]) {
+    if (!valid) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ro[q] = GA_NOROW;
+      return;
+    }
+    const int64_t r0 = t.i0 + 64 * wave + (lane >> 3);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t row = r0 + 8 * q;
+      const int64_t at = t.seg0 + row;
+      const uint32_t v = (uint32_t)arow[at < M ? at : M - 1];
+      ro[q] = row < t.nrows ? v : GA_NOROW;
+    }
+  };
+  auto gather_offsets = [&](uint32_t (&ro)[8]) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      ro[q] = ro[q] == GA_NOROW ? GA_NOROW : ro[q] * (uint32_t)(lda * 2);
+  };
+  if constexpr (GA) {
+    gather_rows(tc, true, ro_cur);
+    gather_rows(tn, has_next, ro_nxt);  // converted in the first k-tile
+    TT_WAIT_VMCNT(0);
+    gather_offsets(ro_cur);
+  }
   i32x4 ra_cur = rsrc_a(tc, true), rb_cur = rsrc_b(tc, true);
   i32x4 ra_nxt = rsrc_a(tn, has_next), rb_nxt = rsrc_b(tn, has_next);
   const int kvalid = (int)R;
@@ -1081,6 +1123,12 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     uint32_t vb = (qq & 1) ? vodd[op] : vbase[op];
     asm volatile("" : "+v"(vb));  // one register per base, not one per chunk
     uint32_t off = vb + ((uint32_t)(qq >> 1) * qstep[op] + (uint32_t)k * kstep[op]);
+    if constexpr (GA) {
+      // The row's source offset plus the lane's chunk and the k-tile.
+      if (is_a)
+        off = (nxt ? ro_nxt[qq] : ro_cur[qq]) + (uint32_t)(2 * ((qq & 1) ? kof_odd : kof)) +
+              (uint32_t)k * kstep[op];
+    }
     if constexpr (KMASK) {
       if (kmaj && k * P_BK + ((qq & 1) ? kof_odd : kof) >= kvalid) off = DM_OOB;
     }
@@ -1187,6 +1235,9 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       }
     }
     TT_WAIT_VMCNT(0);
+    if constexpr (GA) {
+      if (FIRST) gather_offsets(ro_nxt);  // the next tile's rows have arrived
+    }
     if constexpr (WG) {
       // The claimed ticket has returned (the wait above covers it); the
       // barrier publishes it, and the next tile is decoded before this
@@ -1267,11 +1318,16 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     nkt_c = nkt_n;
     ra_cur = ra_nxt;
     rb_cur = rb_nxt;
+    if constexpr (GA) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ro_cur[q] = ro_nxt[q];
+    }
     if constexpr (!WG) {
       has_next = n + 2 < ntiles;
       if (has_next)
         tile_at<MODE, TRANS_B, 2>(pos + (n + 2) * G, p0, p1, out, K, N, E, tiles_j, row_start,
                                   tile_start, tn);
+      if constexpr (GA) gather_rows(tn, has_next, ro_nxt);
       ra_nxt = rsrc_a(tn, has_next);
       rb_nxt = rsrc_b(tn, has_next);
     } else {
@@ -2098,12 +2154,13 @@ int cu_count() {
 // ranking of wgrad.
 size_t p64_schedule_bytes(int E) { return schedule_bytes(E) + (size_t)E * sizeof(int); }
 
-template <int MODE, bool TB, int ET, bool KMASK>
+template <int MODE, bool TB, int ET, bool KMASK, bool GA = false>
 int launch_p64_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
-                 int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj) {
+                 int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj,
+                 const int32_t* arow = nullptr, int64_t asrc_rows = 0) {
   const size_t lds = p64_schedule_bytes(E);  // stages and epilogue staging are static LDS
   static size_t allowed = 64 * 1024;
-  const int rc = allow_lds(&gmm_p64_kernel<MODE, TB, ET, KMASK>, lds, allowed);
+  const int rc = allow_lds(&gmm_p64_kernel<MODE, TB, ET, KMASK, GA>, lds, allowed);
   if (rc != TT_OK) return rc;
   int slot = 0;
   if constexpr (MODE == MODE_WGRAD) {
@@ -2116,9 +2173,10 @@ int launch_p64_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K
   }
   const int64_t cus = cu_count();
   const int64_t grid = nblk < cus ? nblk : cus;
-  hipLaunchKernelGGL((gmm_p64_kernel<MODE, TB, ET, KMASK>), dim3((unsigned)grid), dim3(DM_NT),
-                     lds, s, static_cast<const char*>(p0), static_cast<const char*>(p1),
-                     static_cast<char*>(out), M, K, N, E, counts, ti, tj, slot);
+  hipLaunchKernelGGL((gmm_p64_kernel<MODE, TB, ET, KMASK, GA>), dim3((unsigned)grid),
+                     dim3(DM_NT), lds, s, static_cast<const char*>(p0),
+                     static_cast<const char*>(p1), static_cast<char*>(out), M, K, N, E, counts,
+                     ti, tj, slot, arow, asrc_rows);
   return tt_check_launch("gmm");
 }
 
@@ -2163,6 +2221,32 @@ int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K,
   if (MODE != MODE_WGRAD && R % DM_BK)
     return launch_mfma_k<MODE, TB, ET, true>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
   return launch_mfma_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
+}
+
+// fwd / dgrad with gathered A rows (persistent kernel only): A row r is row
+// arow[r] of src ([src_rows, R], R the reduction length).
+template <int MODE, bool TB, int ET>
+int launch_gather(const void* src, int64_t src_rows, const int32_t* arow, const void* w, void* out,
+                  int64_t M, int64_t K, int64_t N, int E, const int64_t* counts, hipStream_t s) {
+  int ti, tj;
+  const int64_t nblk = grid_blocks(MODE, TB, M, K, N, E, DM_BM, DM_BN, ti, tj);
+  if (nblk == 0) return TT_OK;
+  TT_REQUIRE(nblk < 0x7fffffff, "gmm: grid too large");
+  const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length = source row length
+  const int64_t J = MODE == MODE_FWD ? N : K;  // output width
+  TT_REQUIRE(R > P_BK && R % P_BK == 0,
+             "gmm gather: the reduction length must be a multiple of %d above %d (got %lld)",
+             P_BK, P_BK, (long long)R);
+  TT_REQUIRE(p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI <= 160 * 1024,
+             "gmm gather: too many experts for the LDS tile schedule");
+  TT_REQUIRE(src_rows >= 1 && (src_rows * R + 4 * P_BK) * 2 < (int64_t)GA_NOROW,
+             "gmm gather: the source must hold at least one row and less than 2 GiB");
+  TT_REQUIRE((M + DM_BM) * J * 2 < (int64_t)DM_OOB && K * N * 2 < (int64_t)DM_OOB &&
+                 (R + 2 * P_BK) * J * 2 < (int64_t)DM_OOB,
+             "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
+             (long long)M, (long long)K, (long long)N);
+  return launch_p64_k<MODE, TB, ET, false, true>(src, w, out, M, K, N, E, counts, s, nblk, ti, tj,
+                                                 arow, src_rows);
 }
 
 template <int MODE, bool KMASK>
@@ -2280,6 +2364,30 @@ int dispatch(const void* p0, const void* p1, int dtype, int64_t m, int64_t k, in
   return launch_mfma<MODE, false, TT_F16>(p0, p1, out, m, k, n, E, counts, s);
 }
 
+template <int MODE>
+int dispatch_gather(const void* src, int64_t src_rows, const int32_t* arow, const void* w,
+                    int dtype, int64_t m, int64_t k, int64_t n, int E, int tb,
+                    const int64_t* counts, void* out, void* stream) {
+  TT_REQUIRE(m >= 0 && k >= 0 && n >= 0, "gmm: negative sizes");
+  TT_REQUIRE(E >= 1 && E <= 4096, "gmm: num_experts must be in [1, 4096]");
+  TT_REQUIRE(dtype == TT_BF16 || dtype == TT_F16, "gmm gather: unsupported dtype %d", dtype);
+  TT_REQUIRE(k % 8 == 0 && n % 8 == 0, "gmm: K and N must be multiples of 8 (got %lld, %lld)",
+             (long long)k, (long long)n);
+  TT_REQUIRE(((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(w) |
+               reinterpret_cast<uintptr_t>(out)) & 15) == 0,
+             "gmm: operands must be 16-byte aligned");
+  TT_REQUIRE(m == 0 || arow != nullptr, "gmm gather: row map required");
+  hipStream_t s = S(stream);
+  auto go = [&](auto tb_c, auto et_c) {
+    return launch_gather<MODE, decltype(tb_c)::value, decltype(et_c)::value>(
+        src, src_rows, arow, w, out, m, k, n, E, counts, s);
+  };
+  using BF = std::integral_constant<int, TT_BF16>;
+  using HF = std::integral_constant<int, TT_F16>;
+  if (dtype == TT_BF16) return tb ? go(std::true_type{}, BF{}) : go(std::false_type{}, BF{});
+  return tb ? go(std::true_type{}, HF{}) : go(std::false_type{}, HF{});
+}
+
 }  // namespace
 
 extern "C" int tt_gmm_fwd(const void* x, const void* w, int dtype, int64_t m, int64_t k,
@@ -2329,4 +2437,20 @@ extern "C" int tt_gmm_fp8_dgrad(const void* dy, const uint8_t* qw, const void* s
   if (rc != TT_OK) return rc;
   return launch_fp8<MODE_DGRAD>(dy, qw, scale, scale_dtype, dx, m, k, n, num_experts, counts,
                                S(stream));
+}
+
+extern "C" int tt_gmm_fwd_gather(const void* x_src, int64_t src_rows, const int32_t* src_of_row,
+                                 const void* w, int dtype, int64_t m, int64_t k, int64_t n,
+                                 int32_t num_experts, int32_t trans_b, const int64_t* counts,
+                                 void* y, void* stream) {
+  return dispatch_gather<MODE_FWD>(x_src, src_rows, src_of_row, w, dtype, m, k, n, num_experts,
+                                   trans_b, counts, y, stream);
+}
+
+extern "C" int tt_gmm_dgrad_gather(const void* dy_src, int64_t src_rows,
+                                   const int32_t* src_of_row, const void* w, int dtype, int64_t m,
+                                   int64_t k, int64_t n, int32_t num_experts, int32_t trans_b,
+                                   const int64_t* counts, void* dx, void* stream) {
+  return dispatch_gather<MODE_DGRAD>(dy_src, src_rows, src_of_row, w, dtype, m, k, n,
+                                     num_experts, trans_b, counts, dx, stream);
 }
