@@ -276,6 +276,16 @@ int tt_gmm_dgrad_gather(const void* dy_src, int64_t src_rows, const int32_t* src
                         const void* w, int dtype, int64_t m, int64_t k, int64_t n,
                         int32_t num_experts, int32_t trans_b, const int64_t* counts, void* dx,
                         void* stream);
+/* wgrad with the rows of x or of dy gathered (exactly one of the two row maps
+ * non-NULL; the other operand is packed [m, k] / [m, n]): x_src
+ * [x_src_rows, k] or dy_src [dy_src_rows, n]. Equals tt_gmm_wgrad on the
+ * gathered rows bit for bit. Long expert reductions only (m > 512 *
+ * num_experts, the four-stage kernel); other problems return
+ * TT_ERR_INVALID. */
+int tt_gmm_wgrad_gather(const void* x, int64_t x_src_rows, const int32_t* x_src_of_row,
+                        const void* dy, int64_t dy_src_rows, const int32_t* dy_src_of_row,
+                        int dtype, int64_t m, int64_t k, int64_t n, int32_t num_experts,
+                        int32_t trans_b, const int64_t* counts, void* dw, void* stream);
 
 /* FP8 e4m3 weights with 128x128 block scales, HF [out, in] orientation:
  * qw [E, N, K] bytes, scale [E, ceil(N/128), ceil(K/128)] (bf16 or f32).

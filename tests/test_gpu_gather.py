@@ -83,3 +83,65 @@ def test_gather_rejects_reductions_it_does_not_cover():
     with pytest.raises(ValueError, match="multiple of 64"):
         _lib.call("tt_gmm_fwd_gather", _lib.ptr(xs), 8, _lib.ptr(rows), _lib.ptr(w), 1, 8, 96, 64,
                   2, 0, _lib.ptr(counts), _lib.ptr(y), _lib.stream())
+
+
+# dtype, trans_b, gathered operand, E, M, T, K, N (more than 512 rows per expert on average)
+WGRAD_CASES = [
+    (torch.bfloat16, False, "x", 64, 65536, 8192, 2048, 1536),
+    (torch.bfloat16, False, "dy", 64, 65536, 8192, 768, 2048),
+    (torch.bfloat16, True, "x", 16, 12000, 3000, 512, 768),
+    (torch.bfloat16, True, "dy", 16, 12000, 3000, 512, 768),
+    (torch.float16, False, "dy", 13, 9000, 2000, 256, 512),
+]
+
+
+@pytest.mark.parametrize("dtype,trans_b,which,E,M,T,K,N", WGRAD_CASES,
+                         ids=lambda v: str(v).replace("torch.", ""))
+def test_gathered_wgrad_equals_the_packed_wgrad(dtype, trans_b, which, E, M, T, K, N):
+    """tt_gmm_wgrad_gather with the rows of x or of dy gathered equals tt_gmm_wgrad on the
+    gathered rows bit for bit (Zipf loads with empty and one-row experts, so some
+    reductions end inside a k-tile and some experts have none)."""
+    from torchturbo_amd import _lib
+
+    counts = _loads(E, M, seed=3 * E + N)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    rows = torch.randint(0, T, (M,), generator=g, device=DEV, dtype=torch.int32)
+    if which == "x":
+        src = torch.randn(T, K, generator=g, device=DEV).to(dtype)
+        other = torch.randn(M, N, generator=g, device=DEV).to(dtype)
+        x_p, dy_p = src[rows.long()], other
+    else:
+        src = torch.randn(T, N, generator=g, device=DEV).to(dtype)
+        other = torch.randn(M, K, generator=g, device=DEV).to(dtype)
+        x_p, dy_p = other, src[rows.long()]
+    wshape = (E, N, K) if trans_b else (E, K, N)
+    cnt = counts.to(DEV)
+    tail = (_lib.dtype_code(dtype), M, K, N, E, int(trans_b), _lib.ptr(cnt))
+    st = _lib.stream()
+    dw_p = torch.empty(wshape, dtype=dtype, device=DEV)
+    _lib.call("tt_gmm_wgrad", _lib.ptr(x_p), _lib.ptr(dy_p), *tail, _lib.ptr(dw_p), st)
+    for _ in range(2):
+        dw_g = torch.full(wshape, float("nan"), dtype=dtype, device=DEV)
+        if which == "x":
+            _lib.call("tt_gmm_wgrad_gather", _lib.ptr(src), T, _lib.ptr(rows), _lib.ptr(other),
+                      0, None, *tail, _lib.ptr(dw_g), st)
+        else:
+            _lib.call("tt_gmm_wgrad_gather", _lib.ptr(other), 0, None, _lib.ptr(src), T,
+                      _lib.ptr(rows), *tail, _lib.ptr(dw_g), st)
+        torch.cuda.synchronize()
+        assert torch.equal(dw_g, dw_p)
+
+
+def test_gathered_wgrad_rejects_short_reductions():
+    """At most 512 rows per expert on average the persistent weight-gradient kernel
+    runs, which has no gathered path: the call fails before any launch."""
+    from torchturbo_amd import _lib
+
+    counts = torch.tensor([300, 200], device=DEV)
+    src = torch.zeros(10, 128, dtype=torch.bfloat16, device=DEV)
+    rows = torch.zeros(500, dtype=torch.int32, device=DEV)
+    dy = torch.zeros(500, 128, dtype=torch.bfloat16, device=DEV)
+    dw = torch.empty(2, 128, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="512 rows"):
+        _lib.call("tt_gmm_wgrad_gather", _lib.ptr(src), 10, _lib.ptr(rows), _lib.ptr(dy), 0, None,
+                  1, 500, 128, 128, 2, 0, _lib.ptr(counts), _lib.ptr(dw), _lib.stream())

@@ -357,6 +357,14 @@ __device__ __forceinline__ void dma16(uint32_t voff, i32x4 rsrc, uint32_t lds_ad
                : "memory");
 }
 
+// One dword per lane into LDS at m0 + 4 lane (row indices of a gathered operand).
+__device__ __forceinline__ void dma4(uint32_t voff, i32x4 rsrc, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_addr_of(lds_char* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
@@ -483,15 +491,25 @@ __device__ __forceinline__ void store_wave_tile(const f32x16 (&acc)[4][4], const
 // operand only feeds output rows/columns that are never stored. The
 // reduction tail of a K-major operand whose length is not a multiple of 32
 // (KMASK) is masked explicitly.
-template <int MODE, bool TRANS_B, int ET, bool KMASK>
+// GX (weight gradients): 0, or 1 / 2 when the rows of x (p0) / dy (p1) are
+// gathered, row r of the expert-packed order being row grow[r] of that
+// operand's source ([gsrc_rows, K] / [gsrc_rows, N]).
+template <int MODE, bool TRANS_B, int ET, bool KMASK, int GX = 0>
 __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict__ p0,
                                                          const char* __restrict__ p1,
                                                          char* __restrict__ out, int64_t M,
                                                          int64_t K, int64_t N, int E,
                                                          const int64_t* __restrict__ counts,
-                                                         int tiles_i, int tiles_j) {
+                                                         int tiles_i, int tiles_j,
+                                                         const int32_t* __restrict__ grow,
+                                                         int64_t gsrc_rows) {
   typedef Layout<MODE, TRANS_B> Lay;
   constexpr int WT = 128, FM = 4, FN = 4;
+  constexpr bool GATH = GX != 0;
+  static_assert(!GATH || (MODE == MODE_WGRAD && !KMASK), "gathered rows: weight gradients only");
+  // Gathered operand: per wave, two groups of four k-tiles of source row
+  // indices (lane i of a group: k-tile i / 16, k-row 2 (8 wv + i % 8) + i / 8 % 2).
+  __shared__ __align__(16) int gidx[GATH ? 2 * 2 * 64 : 4];
   // One static LDS array per stage and a k-loop unrolled by the stage count:
   // every address is then a compile-time stage base plus a lane offset.
   __shared__ __align__(16) char stage0[DM_STAGE];
@@ -514,6 +532,8 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   const bool a_role = wave < 2;
   const int wv = wave & 1;
   const int nkt = (int)((t.R + DM_BK - 1) / DM_BK);
+  // The waves that load the gathered operand (x is A unless TRANS_B).
+  const bool gath = GATH && (a_role == ((GX == 1) != TRANS_B));
 
   // This wave's operand: buffer resource, per-chunk byte offsets at k-tile 0
   // and the per-k-tile advance.
@@ -524,6 +544,10 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   int64_t obytes;
   if (a_role) obytes = (Lay::A_K ? t.nrows : t.R) * t.lda * 2;
   else obytes = (MODE == MODE_WGRAD) ? t.R * t.ldb * 2 : K * N * 2;
+  if (gath) {  // the whole source
+    obase = GX == 1 ? p0 : p1;
+    obytes = gsrc_rows * ld * 2;
+  }
   const i32x4 rsrc = make_rsrc(obase, obytes);
   uint32_t voff[8];
   int kof[8];
@@ -550,11 +574,48 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   const uint32_t dst_wave = (a_role ? 0u : (uint32_t)DM_TILE) + (uint32_t)wv * 8192u;
   const int kvalid = (int)t.R;
 
+  // Gathered operand: the k-tile's source rows come through the LDS index
+  // ring (a group of four k-tiles per dword DMA, issued four k-tiles ahead of
+  // its first use so the pipeline's waits cover it); each chunk's offset is
+  // its source row's plus the lane's column chunk (two, by k-row parity).
+  // Reduction rows past the expert's end read as zeros.
+  uint32_t gof[8], gcol[2];
+  const i32x4 irsrc = make_rsrc(grow, GATH ? M * 4 : 0);
+  if constexpr (GATH) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int c = (lane & 31) ^ (4 * ((2 * p + (lane >> 5)) & 3));
+      gcol[p] = (uint32_t)((orow0 + 8 * c) * 2);
+    }
+  }
+  auto issue_idx = [&](int grp) {
+    const int j = lane >> 4, h = (lane >> 3) & 1, q = lane & 7;
+    const int64_t row = (int64_t)(4 * grp + j) * DM_BK + 2 * (wv * 8 + q) + h;
+    dma4((uint32_t)((t.seg0 + row) * 4), irsrc,
+         lds_addr_of((lds_char*)gidx) + (uint32_t)((wv * 2 + (grp & 1)) * 256));
+  };
+  auto gather_offsets = [&](int kk) {
+    const int h = lane >> 5;
+    lds_char* const ring = (lds_char*)gidx + (wv * 2 + ((kk >> 2) & 1)) * 256;
+    const uint32_t at = (uint32_t)(((kk & 3) * 16 + h * 8) * 4);
+    const uint4 i0 = read_k(ring, at), i1 = read_k(ring, at + 16);
+    const uint32_t idx[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+    const uint32_t ld2 = (uint32_t)(ld * 2);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t row = (int64_t)kk * DM_BK + 2 * (wv * 8 + q) + h;
+      gof[q] = row < t.R ? idx[q] * ld2 + gcol[q & 1] : DM_OOB;
+    }
+  };
+
   // Chunk q of k-tile kt into stage `stg`.
   auto issue_one = [&](lds_char* stg, int kt, int q) {
     uint32_t off = voff[q] + (uint32_t)kt * kstep;
     if constexpr (KMASK) {
       if (kmaj && kt * DM_BK + kof[q] >= kvalid) off = DM_OOB;
+    }
+    if constexpr (GATH) {
+      if (gath) off = gof[q];
     }
     dma16(off, rsrc, lds_addr_of(stg) + dst_wave + (uint32_t)q * 1024u);
   };
@@ -628,6 +689,14 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
     }
     TT_WAIT_VMCNT(8);
     __builtin_amdgcn_s_barrier();
+    if constexpr (GATH) {
+      if (gath) {
+        // Indices of k-tiles kt + 4 .. kt + 7 go out before this step's loads,
+        // so the next step's wait covers them.
+        if ((kt & 3) == 0) issue_idx((kt >> 2) + 1);
+        gather_offsets(kt + 3);
+      }
+    }
     refresh();
 #pragma unroll
     for (int i = 0; i < FM * FN; ++i) {
@@ -638,9 +707,21 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
     }
   };
 
-  issue(s0, 0);
-  issue(s1, 1);
-  issue(s2, 2);
+  if constexpr (GATH) {
+    if (gath) {
+      issue_idx(0);
+      TT_WAIT_VMCNT(0);
+    }
+  }
+  auto issue_first = [&](lds_char* stg, int kk) {
+    if constexpr (GATH) {
+      if (gath) gather_offsets(kk);
+    }
+    issue(stg, kk);
+  };
+  issue_first(s0, 0);
+  issue_first(s1, 1);
+  issue_first(s2, 2);
   TT_WAIT_VMCNT(16);
   __builtin_amdgcn_s_barrier();
   refresh();
@@ -2117,20 +2198,22 @@ int allow_lds(F* kernel, size_t lds, size_t& allowed) {
   return TT_OK;
 }
 
-template <int MODE, bool TB, int ET, bool KMASK>
+template <int MODE, bool TB, int ET, bool KMASK, int GX = 0>
 int launch_mfma_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
-                  int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj) {
+                  int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj,
+                  const int32_t* grow = nullptr, int64_t gsrc_rows = 0) {
   // Weight gradients on XCD pairs: eight blocks per group of eight expert
   // ranks and tile (see describe_tile).
   if (MODE == MODE_WGRAD && wgrad_pair_split(ti, tj) != 0)
     nblk = 8 * (int64_t)((E + 7) / 8) * ti * tj;
   const size_t lds = schedule_bytes(E);  // the stages are static LDS
   static size_t allowed = 64 * 1024;
-  const int rc = allow_lds(&gmm_mfma_kernel<MODE, TB, ET, KMASK>, lds, allowed);
+  const int rc = allow_lds(&gmm_mfma_kernel<MODE, TB, ET, KMASK, GX>, lds, allowed);
   if (rc != TT_OK) return rc;
-  hipLaunchKernelGGL((gmm_mfma_kernel<MODE, TB, ET, KMASK>), dim3((unsigned)nblk), dim3(DM_NT),
-                     lds, s, static_cast<const char*>(p0), static_cast<const char*>(p1),
-                     static_cast<char*>(out), M, K, N, E, counts, ti, tj);
+  hipLaunchKernelGGL((gmm_mfma_kernel<MODE, TB, ET, KMASK, GX>), dim3((unsigned)nblk),
+                     dim3(DM_NT), lds, s, static_cast<const char*>(p0),
+                     static_cast<const char*>(p1), static_cast<char*>(out), M, K, N, E, counts,
+                     ti, tj, grow, gsrc_rows);
   return tt_check_launch("gmm");
 }
 
@@ -2247,6 +2330,35 @@ int launch_gather(const void* src, int64_t src_rows, const int32_t* arow, const 
              (long long)M, (long long)K, (long long)N);
   return launch_p64_k<MODE, TB, ET, false, true>(src, w, out, M, K, N, E, counts, s, nblk, ti, tj,
                                                  arow, src_rows);
+}
+
+// Weight gradients with the rows of x (GX 1) or dy (GX 2) gathered from a
+// source of src_rows rows; the long-reduction kernel only (more than 512 rows
+// per expert on average), where the layer's packed copies would be read.
+template <bool TB, int ET, int GX>
+int launch_wgrad_gather(const void* x, const void* dy, int64_t src_rows, const int32_t* grow,
+                        void* dw, int64_t M, int64_t K, int64_t N, int E, const int64_t* counts,
+                        hipStream_t s) {
+  int ti, tj;
+  const int64_t nblk = grid_blocks(MODE_WGRAD, TB, M, K, N, E, DM_BM, DM_BN, ti, tj);
+  if (nblk == 0) return TT_OK;
+  TT_REQUIRE(nblk < 0x7fffffff, "gmm: grid too large");
+  TT_REQUIRE(M > (int64_t)E * P_WGRAD_ROWS,
+             "gmm gather: weight gradients with gathered rows need more than %lld rows per "
+             "expert on average (M=%lld, E=%d)",
+             (long long)P_WGRAD_ROWS, (long long)M, E);
+  TT_REQUIRE(schedule_bytes(E) + (size_t)DM_ST * DM_STAGE + 1024 <= 160 * 1024,
+             "gmm: too many experts for the LDS tile schedule");
+  const int64_t ld = K > N ? K : N;
+  const int64_t gld = GX == 1 ? K : N;
+  TT_REQUIRE((M + DM_BM) * ld * 2 < (int64_t)DM_OOB && K * N * 2 < (int64_t)DM_OOB &&
+                 M * 4 < (int64_t)DM_OOB,
+             "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
+             (long long)M, (long long)K, (long long)N);
+  TT_REQUIRE(src_rows >= 1 && (src_rows + 1) * gld * 2 < (int64_t)DM_OOB,
+             "gmm gather: the source must hold at least one row and less than 4 GiB");
+  return launch_mfma_k<MODE_WGRAD, TB, ET, false, GX>(x, dy, dw, M, K, N, E, counts, s, nblk, ti,
+                                                      tj, grow, src_rows);
 }
 
 template <int MODE, bool KMASK>
@@ -2388,6 +2500,40 @@ int dispatch_gather(const void* src, int64_t src_rows, const int32_t* arow, cons
   return tb ? go(std::true_type{}, HF{}) : go(std::false_type{}, HF{});
 }
 
+int dispatch_wgrad_gather(const void* x, int64_t x_src_rows, const int32_t* x_rows,
+                          const void* dy, int64_t dy_src_rows, const int32_t* dy_rows, int dtype,
+                          int64_t m, int64_t k, int64_t n, int E, int tb, const int64_t* counts,
+                          void* dw, void* stream) {
+  TT_REQUIRE(m >= 0 && k >= 0 && n >= 0, "gmm: negative sizes");
+  TT_REQUIRE(E >= 1 && E <= 4096, "gmm: num_experts must be in [1, 4096]");
+  TT_REQUIRE(dtype == TT_BF16 || dtype == TT_F16, "gmm gather: unsupported dtype %d", dtype);
+  TT_REQUIRE(k % 8 == 0 && n % 8 == 0, "gmm: K and N must be multiples of 8 (got %lld, %lld)",
+             (long long)k, (long long)n);
+  TT_REQUIRE((x_rows != nullptr) != (dy_rows != nullptr),
+             "gmm gather: exactly one of the two row maps must be given");
+  TT_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
+               reinterpret_cast<uintptr_t>(dw)) & 15) == 0,
+             "gmm: operands must be 16-byte aligned");
+  hipStream_t s = S(stream);
+  const int32_t* rows = x_rows ? x_rows : dy_rows;
+  const int64_t src = x_rows ? x_src_rows : dy_src_rows;
+  auto go = [&](auto tb_c, auto et_c, auto gx_c) {
+    return launch_wgrad_gather<decltype(tb_c)::value, decltype(et_c)::value,
+                               decltype(gx_c)::value>(x, dy, src, rows, dw, m, k, n, E, counts,
+                                                      s);
+  };
+  using BF = std::integral_constant<int, TT_BF16>;
+  using HF = std::integral_constant<int, TT_F16>;
+  using GXX = std::integral_constant<int, 1>;
+  using GDY = std::integral_constant<int, 2>;
+  if (dtype == TT_BF16) {
+    if (x_rows) return tb ? go(std::true_type{}, BF{}, GXX{}) : go(std::false_type{}, BF{}, GXX{});
+    return tb ? go(std::true_type{}, BF{}, GDY{}) : go(std::false_type{}, BF{}, GDY{});
+  }
+  if (x_rows) return tb ? go(std::true_type{}, HF{}, GXX{}) : go(std::false_type{}, HF{}, GXX{});
+  return tb ? go(std::true_type{}, HF{}, GDY{}) : go(std::false_type{}, HF{}, GDY{});
+}
+
 }  // namespace
 
 extern "C" int tt_gmm_fwd(const void* x, const void* w, int dtype, int64_t m, int64_t k,
@@ -2453,4 +2599,13 @@ extern "C" int tt_gmm_dgrad_gather(const void* dy_src, int64_t src_rows,
                                    const int64_t* counts, void* dx, void* stream) {
   return dispatch_gather<MODE_DGRAD>(dy_src, src_rows, src_of_row, w, dtype, m, k, n,
                                      num_experts, trans_b, counts, dx, stream);
+}
+
+extern "C" int tt_gmm_wgrad_gather(const void* x, int64_t x_src_rows, const int32_t* x_src_of_row,
+                                   const void* dy, int64_t dy_src_rows,
+                                   const int32_t* dy_src_of_row, int dtype, int64_t m, int64_t k,
+                                   int64_t n, int32_t num_experts, int32_t trans_b,
+                                   const int64_t* counts, void* dw, void* stream) {
+  return dispatch_wgrad_gather(x, x_src_rows, x_src_of_row, dy, dy_src_rows, dy_src_of_row, dtype,
+                               m, k, n, num_experts, trans_b, counts, dw, stream);
 }
