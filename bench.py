@@ -4,7 +4,10 @@
 One step = routing (top-k softmax) -> permute -> fc1 grouped GEMM -> SwiGLU x
 probs -> fc2 grouped GEMM -> unpermute, forward and backward, on one batch of
 synthetic inputs already resident in HBM (``MoELayer.forward_with_logits``
-with every op served by the HIP providers). Default workload: the
+with every op served by the HIP providers). On one GPU the layer folds the
+permutation into fc1 and the unpermutation's backward into fc2's gradients
+(the GEMMs gather token rows through the routing index), when the shapes
+allow: the Qwen, Mixtral and varlen layers. Default workload: the
 Qwen3-30B-A3B-shaped layer (16384 tokens, hidden 2048, 128 experts, top-8,
 ffn 768, bf16, Zipf-skewed fp32 router logits).
 
@@ -33,7 +36,8 @@ if ROOT not in sys.path:
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 HBM_PEAK_GBS = 8000.0
-GEMM_ENTRIES = ("tt_gmm_fwd", "tt_gmm_dgrad", "tt_gmm_wgrad", "tt_gmm_fp8_fwd", "tt_gmm_fp8_dgrad")
+GEMM_ENTRIES = ("tt_gmm_fwd", "tt_gmm_dgrad", "tt_gmm_wgrad", "tt_gmm_fwd_gather",
+                "tt_gmm_dgrad_gather", "tt_gmm_wgrad_gather", "tt_gmm_fp8_fwd", "tt_gmm_fp8_dgrad")
 PERMUTE_ENTRIES = ("tt_permute_scatter", "tt_unpermute_gather")
 ROUTER_ENTRIES = ("tt_router_gate_fwd", "tt_router_topk_fwd", "tt_router_topk_bwd",
                   "tt_router_loss_fwd", "tt_router_loss_bwd")
@@ -345,7 +349,8 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "grouped GEMM (tt_gmm_*; fc1/fc2 fwd, dgrad, wgrad)",
+            "kernel": "grouped GEMM (tt_gmm_*, row-gathering ones included; fc1/fc2 fwd, "
+                      "dgrad, wgrad)",
             "achieved": round(achieved_tflops, 1),
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
@@ -359,6 +364,7 @@ def main():
         "permute": {
             "bound": "hbm", "unit": "GB/s", "peak": HBM_PEAK_GBS,
             "permute_scatter_gbs": None if perm_gbs is None else round(perm_gbs, 1),
+            "permute_scatter_calls_per_step": perm_n / args.steps,
             "unpermute_gather_gbs": None if unperm_gbs is None else round(unperm_gbs, 1),
             "bytes_per_pass": pass_bytes,
         },

@@ -145,3 +145,50 @@ def test_gathered_wgrad_rejects_short_reductions():
     with pytest.raises(ValueError, match="512 rows"):
         _lib.call("tt_gmm_wgrad_gather", _lib.ptr(src), 10, _lib.ptr(rows), _lib.ptr(dy), 0, None,
                   1, 500, 128, 128, 2, 0, _lib.ptr(counts), _lib.ptr(dw), _lib.stream())
+
+
+def _run_layer(layer, hidden, logits, grad):
+    for p in layer.parameters():
+        p.grad = None
+    hd = hidden.clone().requires_grad_()
+    ld = logits.clone().requires_grad_()
+    out = layer.forward_with_logits(hd, ld)
+    out.backward(grad)
+    return (out.detach(), hd.grad, ld.grad, layer.experts.weight1.grad.clone(),
+            layer.experts.weight2.grad.clone(), layer.token_dispatcher.tokens_per_expert.clone())
+
+
+@pytest.mark.parametrize("tokens,hidden,ffn,experts,topk,logits", [
+    (4096, 512, 256, 16, 4, "zipf"),
+    (4096, 1024, 384, 8, 2, "normal"),
+])
+def test_layer_gathering_experts_equal_the_dispatched_path(process_ops, monkeypatch, tokens,
+                                                           hidden, ffn, experts, topk, logits):
+    """MoELayer with the permutation and unpermutation folded into the GEMMs (the
+    default on one GPU when the shapes allow) gives the output, every gradient and the
+    per-expert counts of the permute -> GroupedMLP -> unpermute path bit for bit."""
+    from dataclasses import replace
+
+    from tests.test_gpu_layer import build_layer
+    from torchturbo_amd import configs as C
+    from torchturbo_amd.dispatch import OpPolicy
+    from torchturbo_amd.runtime import CudaRuntime
+
+    process_ops(CudaRuntime(), OpPolicy.CUSTOM)
+    w = replace(C.QWEN3, tokens=tokens, hidden=hidden, ffn=ffn, experts=experts, topk=topk,
+                logits=logits)
+    hidden_t = C.make_hidden(w).to(DEV)
+    logits_t = C.make_logits(w).to(DEV)
+    w1, w2 = C.make_weights(w)
+    grad = C.make_grad(w).to(DEV)
+    layer = build_layer(w, w1, w2)
+    flat = hidden_t.view(-1, hidden)
+    ids = logits_t.topk(topk, dim=1).indices
+    monkeypatch.setenv("TORCHTURBO_AMD_FUSED_PERMUTE", "1")
+    assert layer._gathering_experts(flat, ids)
+    fused = _run_layer(layer, hidden_t, logits_t, grad)
+    monkeypatch.setenv("TORCHTURBO_AMD_FUSED_PERMUTE", "0")
+    assert not layer._gathering_experts(flat, ids)
+    plain = _run_layer(layer, hidden_t, logits_t, grad)
+    for a, b, name in zip(fused, plain, ("out", "d_hidden", "d_logits", "d_w1", "d_w2", "counts")):
+        assert torch.equal(a, b), name

@@ -575,11 +575,16 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   const int kvalid = (int)t.R;
 
   // Gathered operand: the k-tile's source rows come through the LDS index
-  // ring (a group of four k-tiles per dword DMA, issued four k-tiles ahead of
-  // its first use so the pipeline's waits cover it); each chunk's offset is
-  // its source row's plus the lane's column chunk (two, by k-row parity).
-  // Reduction rows past the expert's end read as zeros.
-  uint32_t gof[8], gcol[2];
+  // ring (a group of four k-tiles per dword DMA, issued five k-tiles ahead of
+  // its first use so the pipeline's waits cover it). A step reads the rows of
+  // the k-tile it will load at the end of its first half, so the LDS reads
+  // are in flight across the wait and barrier, and turns them into offsets
+  // after the barrier (reading them where the loads go out, or just before
+  // them, was 4-16 % slower): each chunk's offset is its source row's plus
+  // the lane's column chunk (two, by k-row parity). Reduction rows past the
+  // expert's end read as zeros.
+  uint32_t grow_v[8], gof[8], gcol[2];
+  const uint32_t ld2 = (uint32_t)(ld * 2);
   const i32x4 irsrc = make_rsrc(grow, GATH ? M * 4 : 0);
   if constexpr (GATH) {
 #pragma unroll
@@ -594,18 +599,19 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
     dma4((uint32_t)((t.seg0 + row) * 4), irsrc,
          lds_addr_of((lds_char*)gidx) + (uint32_t)((wv * 2 + (grp & 1)) * 256));
   };
-  auto gather_offsets = [&](int kk) {
-    const int h = lane >> 5;
-    lds_char* const ring = (lds_char*)gidx + (wv * 2 + ((kk >> 2) & 1)) * 256;
-    const uint32_t at = (uint32_t)(((kk & 3) * 16 + h * 8) * 4);
-    const uint4 i0 = read_k(ring, at), i1 = read_k(ring, at + 16);
-    const uint32_t idx[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
-    const uint32_t ld2 = (uint32_t)(ld * 2);
+  auto offsets = [&](int kk) {  // byte offsets of k-tile kk's chunks from its rows
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const int64_t row = (int64_t)kk * DM_BK + 2 * (wv * 8 + q) + h;
-      gof[q] = row < t.R ? idx[q] * ld2 + gcol[q & 1] : DM_OOB;
+      const int row = kk * DM_BK + 2 * (wv * 8 + q) + (lane >> 5);
+      gof[q] = row < kvalid ? grow_v[q] * ld2 + gcol[q & 1] : DM_OOB;
     }
+  };
+  auto read_rows = [&](int kk) {  // source rows of k-tile kk's eight chunks
+    lds_char* const ring = (lds_char*)gidx + (wv * 2 + ((kk >> 2) & 1)) * 256;
+    const uint32_t at = (uint32_t)(((kk & 3) * 16 + (lane >> 5) * 8) * 4);
+    const uint4 i0 = read_k(ring, at), i1 = read_k(ring, at + 16);
+    grow_v[0] = i0.x; grow_v[1] = i0.y; grow_v[2] = i0.z; grow_v[3] = i0.w;
+    grow_v[4] = i1.x; grow_v[5] = i1.y; grow_v[6] = i1.z; grow_v[7] = i1.w;
   };
 
   // Chunk q of k-tile kt into stage `stg`.
@@ -685,16 +691,19 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
     for (int i = 0; i < FM * FN; ++i) {
       mfma(i, a0, b0, decltype(first_c)::value);
       if (i < FM + FN) frag(cur, 1, i, a1, b1);
+      if constexpr (GATH) {
+        if (i == FM * FN - 1 && gath) read_rows(kt + 3);  // in flight across the wait
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     TT_WAIT_VMCNT(8);
     __builtin_amdgcn_s_barrier();
     if constexpr (GATH) {
+      // Indices of k-tiles kt + 5 .. kt + 8 go out before this step's loads,
+      // so the next step's wait covers them before step kt + 2 reads them.
       if (gath) {
-        // Indices of k-tiles kt + 4 .. kt + 7 go out before this step's loads,
-        // so the next step's wait covers them.
-        if ((kt & 3) == 0) issue_idx((kt >> 2) + 1);
-        gather_offsets(kt + 3);
+        if ((kt & 3) == 3) issue_idx((kt + 5) >> 2);
+        offsets(kt + 3);
       }
     }
     refresh();
@@ -710,12 +719,16 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   if constexpr (GATH) {
     if (gath) {
       issue_idx(0);
+      issue_idx(1);
       TT_WAIT_VMCNT(0);
     }
   }
   auto issue_first = [&](lds_char* stg, int kk) {
     if constexpr (GATH) {
-      if (gath) gather_offsets(kk);
+      if (gath) {
+        read_rows(kk);
+        offsets(kk);
+      }
     }
     issue(stg, kk);
   };

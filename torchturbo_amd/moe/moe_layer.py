@@ -16,6 +16,8 @@ import torch
 import torch.distributed as dist
 import torch.nn.functional as F
 
+from ..dispatch import ops
+from .experts import GroupedMLP
 from .module import ModuleSpec, build_module
 from .moe_config import MoEConfig
 from .router import TopKRouter
@@ -83,7 +85,47 @@ class MoELayer(BaseMoELayer):
         if self.use_shared_expert:
             self.shared_experts = build_module(submodules.shared_experts, config=config)
 
+    def _gathering_experts(self, tokens, expert_indices) -> bool:
+        """Whether the permutation and unpermutation can be folded into the
+        experts' GEMMs (HIP providers for the three ops, plain ``GroupedMLP``
+        experts; shapes in ``providers.hip.fused_experts.eligible``)."""
+        if type(self.experts) is not GroupedMLP or self.config.moe_apply_probs_on_input:
+            return False
+        if expert_indices is None or not tokens.is_cuda:
+            return False
+        try:
+            chosen = (ops.selected_impl_name("moe_permutation"),
+                      ops.selected_impl_name("grouped_matmul"),
+                      ops.selected_impl_name("moe_unpermutation"))
+        except RuntimeError:
+            return False
+        if chosen != ("hip_moe_mask_permutation", "hip_grouped_matmul",
+                      "hip_moe_mask_unpermutation"):
+            return False
+        from ..providers.hip import fused_experts
+        return fused_experts.eligible(tokens, self.experts.weight1, expert_indices.shape[1],
+                                      self.num_local_experts)
+
     def _experts_and_combine(self, hidden_states, probs, routing_map, expert_indices):
+        flat = hidden_states.view(-1, hidden_states.shape[-1])
+        if self._gathering_experts(flat, expert_indices):
+            # One GPU, every expert local: the GEMMs gather the token rows
+            # themselves (same results, no packed copies).
+            from ..providers.hip import fused_experts
+            tokens, counts = fused_experts.grouped_mlp_tokens(self.experts, flat, probs,
+                                                              routing_map, expert_indices)
+            self.token_dispatcher.tokens_per_expert = counts
+            output = tokens.view(hidden_states.shape).to(hidden_states.dtype)
+        else:
+            output = self._dispatched_experts(hidden_states, probs, routing_map, expert_indices)
+        if self.shared_expert is not None:
+            shared = self.shared_expert(hidden_states)
+            output = output + F.sigmoid(self.shared_expert_gate(hidden_states)) * shared
+        if self.shared_experts is not None:
+            output = output + self.shared_experts(hidden_states)
+        return output
+
+    def _dispatched_experts(self, hidden_states, probs, routing_map, expert_indices):
         d = self.token_dispatcher
         tokens, expert_probs = d.dispatch_preprocess(hidden_states, routing_map, probs,
                                                      expert_indices=expert_indices)
@@ -94,13 +136,7 @@ class MoELayer(BaseMoELayer):
         tokens = d.combine_preprocess(tokens)
         tokens = d.token_combine(tokens)
         tokens = d.combine_postprocess(tokens)
-        output = tokens.to(hidden_states.dtype)
-        if self.shared_expert is not None:
-            shared = self.shared_expert(hidden_states)
-            output = output + F.sigmoid(self.shared_expert_gate(hidden_states)) * shared
-        if self.shared_experts is not None:
-            output = output + self.shared_experts(hidden_states)
-        return output
+        return tokens.to(hidden_states.dtype)
 
     def forward(self, hidden_states, input_ids=None):
         probs, routing_map, expert_indices, logits = self.router(
