@@ -267,7 +267,8 @@ int tt_gmm_wgrad(const void* x, const void* dy, int dtype, int64_t m, int64_t k,
  * ops/providers/native/grouped_matmul.py:16-56), with no packed copy of the
  * activations; the result equals tt_gmm_fwd / tt_gmm_dgrad on the gathered
  * rows bit for bit. bf16 / f16, R a multiple of 64 above 64, sources under
- * 2 GiB; other problems return TT_ERR_INVALID. */
+ * 2 GiB; other problems return TT_ERR_INVALID. A src_of_row entry outside
+ * [0, src_rows) reads a row of zeros (the loads are bounded by the source). */
 int tt_gmm_fwd_gather(const void* x_src, int64_t src_rows, const int32_t* src_of_row,
                       const void* w, int dtype, int64_t m, int64_t k, int64_t n,
                       int32_t num_experts, int32_t trans_b, const int64_t* counts, void* y,
