@@ -191,3 +191,4 @@ def test_hip_providers_registered_for_cuda_only():
                                         "router_loss_stats"}
     assert all(s.devices == (TurboDevice.CUDA,) and s.kind == OpImplKind.CUSTOM
                and s.priority > 100 for s in hip)
+

@@ -107,3 +107,19 @@ def test_softmax_layer_preserves_router_probabilities_and_gradients(process_ops)
         out.sum().backward()
         expected.backward()
         torch.testing.assert_close(layer.router.weight.grad.flatten(), ref_logits.grad)
+
+
+def test_folded_permutation_shape_rule():
+    """Where the layer folds the permutation into the GEMMs (shape rule only; the
+    GPU tests check the results): Qwen3-30B-A3B and the varlen batch yes, Mixtral's
+    wide experts, small batches, fp32 and odd hidden sizes no."""
+    from torchturbo_amd.providers.hip.fused_experts import shapes_pay
+
+    bf = torch.bfloat16
+    assert shapes_pay(16384, 2048, 1536, 8, 128, bf)            # Qwen3-30B-A3B
+    assert shapes_pay(72192, 2048, 1536, 8, 128, bf)            # varlen stress
+    assert not shapes_pay(8192, 4096, 28672, 2, 8, bf)          # Mixtral: fc1 7x hidden
+    assert not shapes_pay(4096, 2048, 1536, 8, 128, bf)         # 256 rows per expert
+    assert not shapes_pay(16384, 2048, 1536, 8, 128, torch.float32)
+    assert not shapes_pay(16384, 2000, 1536, 8, 128, bf)        # hidden not a multiple of 64
+    assert not shapes_pay(16384, 64, 128, 8, 16, bf)            # hidden of one k-tile

@@ -173,13 +173,20 @@ def eligible(tokens: torch.Tensor, w1: torch.Tensor, topk: int, num_experts: int
     gradients with their work, T·k·H·F: on Qwen3-30B-A3B (F 768, H 2048) the
     layer step is 4 % faster, on Mixtral (F 14336, H 4096) it would be 1-3 %
     slower (its weight gradients re-read each gathered row slice many times)."""
-    if not enabled() or not tokens.is_cuda or tokens.dim() != 2:
-        return False
-    if tokens.dtype not in (torch.bfloat16, torch.float16) or w1.dtype != tokens.dtype:
+    if not enabled() or not tokens.is_cuda or tokens.dim() != 2 or w1.dtype != tokens.dtype:
         return False
     T, H = tokens.shape
-    return (H > 64 and H % 64 == 0 and T * topk > 512 * num_experts
-            and w1.shape[-1] <= 2 * H)
+    return shapes_pay(T, H, w1.shape[-1], topk, num_experts, tokens.dtype)
+
+
+def shapes_pay(tokens: int, hidden: int, fc1_width: int, topk: int, num_experts: int,
+               dtype: torch.dtype) -> bool:
+    """The shape part of ``eligible``: 16-bit activations, a hidden size the
+    gathering fwd / dgrad kernel covers (a multiple of 64 above 64), more than
+    512 routed rows per expert on average (the gathering weight-gradient
+    kernel) and fc1 at most twice as wide as the hidden size."""
+    return (dtype in (torch.bfloat16, torch.float16) and hidden > 64 and hidden % 64 == 0
+            and tokens * topk > 512 * num_experts and fc1_width <= 2 * hidden)
 
 
 def grouped_mlp_tokens(experts, tokens, probs, routing_map, expert_indices):
