@@ -192,3 +192,45 @@ def test_layer_gathering_experts_equal_the_dispatched_path(process_ops, monkeypa
     plain = _run_layer(layer, hidden_t, logits_t, grad)
     for a, b, name in zip(fused, plain, ("out", "d_hidden", "d_logits", "d_w1", "d_w2", "counts")):
         assert torch.equal(a, b), name
+
+
+def test_gathering_experts_check_their_routing_input(process_ops):
+    """The folded path runs the same input checks as the dispatched one: with checks on,
+    an out-of-range expert id and a routing map that disagrees with the ids raise
+    ValueError before any GEMM."""
+    from torchturbo_amd import checks
+    from torchturbo_amd.dispatch import OpPolicy
+    from torchturbo_amd.moe import GroupedMLP, MoEConfig
+    from torchturbo_amd.providers.hip import fused_experts
+    from torchturbo_amd.runtime import CudaRuntime
+
+    process_ops(CudaRuntime(), OpPolicy.CUSTOM)
+
+    T, H, F, E, k = 2048, 256, 128, 4, 2  # 1024 rows per expert: the folded path's shapes
+    cfg = MoEConfig(hidden_size=H, num_moe_experts=E, moe_ffn_hidden_size=F,
+                    gated_linear_unit=True, activation_func=torch.nn.functional.silu,
+                    moe_router_topk=k, params_dtype=torch.bfloat16)
+    experts = GroupedMLP(E, False, cfg).to(DEV)
+    with torch.no_grad():
+        experts.weight1.normal_(0, 0.02)
+        experts.weight2.normal_(0, 0.02)
+    tokens = torch.randn(T, H, device=DEV).to(torch.bfloat16)
+    assert fused_experts.eligible(tokens, experts.weight1, k, E)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.rand(T, E, generator=g).topk(k, dim=1).indices
+    rmap = torch.zeros(T, E, dtype=torch.bool).scatter(1, ids, True)
+    probs = torch.rand(T, E).masked_fill(~rmap, 0.0)
+    bad = ids.clone()
+    bad[7, 1] = E
+    other = ids.clone()
+    other[3, 0] = [e for e in range(E) if e not in ids[3].tolist()][0]
+    with checks.checking():
+        with pytest.raises(ValueError, match="1 of 4096 slots"):
+            fused_experts.grouped_mlp_tokens(experts, tokens, probs.to(DEV), rmap.to(DEV),
+                                             bad.to(DEV))
+        with pytest.raises(ValueError, match="disagree for 1 of 2048 tokens"):
+            fused_experts.grouped_mlp_tokens(experts, tokens, probs.to(DEV), rmap.to(DEV),
+                                             other.to(DEV))
+        out, counts = fused_experts.grouped_mlp_tokens(experts, tokens, probs.to(DEV),
+                                                       rmap.to(DEV), ids.to(DEV))
+        assert out.shape == (T, H) and int(counts.sum()) == T * k
