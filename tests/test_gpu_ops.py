@@ -922,6 +922,48 @@ def _zipf_counts(E, M, seed, empty=(3, 17)):
 
 # Shapes of the Qwen3-30B-A3B layer's two GEMMs (fc1: K 2048 -> N 1536, fc2: K 768 ->
 # N 2048), tens of thousands of rows, Zipf loads with empty experts. Each launch has far
+@pytest.mark.parametrize("trans_b", [False, True])
+@pytest.mark.parametrize("E,K,N", [(256, 512, 1536), (96, 320, 768), (40, 256, 1000)])
+def test_grouped_matmul_thin_experts_exact(trans_b, E, K, N):
+    """Many experts of at most 64 rows (their output tiles are taken two per schedule
+    slot by the persistent fwd / dgrad kernel, an odd number of column tiles leaving
+    a slot with one) mixed with larger experts, some of whose last tiles are thin too,
+    into NaN-filled outputs with small-integer operands: every row exact, in blocks
+    that walk thin and full tiles in turn."""
+    from torchturbo_amd import _lib
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    g = torch.Generator().manual_seed(E + K + N)
+    small = torch.randint(1, 65, (E,), generator=g)
+    big = torch.randint(65, 900, (E,), generator=g)
+    counts = torch.where(torch.rand(E, generator=g) < 0.6, small, big)
+    counts[0] = 0
+    counts[1] = 64
+    counts[2] = 65
+    counts[3] = 256 + 64
+    M = int(counts.sum())
+    dtype = torch.bfloat16
+    x = torch.randint(-2, 3, (M, K), generator=g).to(dtype).to(DEV)
+    dy = torch.randint(-2, 3, (M, N), generator=g).to(dtype).to(DEV)
+    wshape = (E, N, K) if trans_b else (E, K, N)
+    w = torch.randint(-2, 3, wshape, generator=g).to(dtype).to(DEV)
+    cnt = counts.to(DEV)
+    args = (_lib.dtype_code(dtype), M, K, N, E, int(trans_b), _lib.ptr(cnt))
+    for rep in range(2):  # the second call into outputs holding the first call's results
+        y = torch.full((M, N), float("nan"), dtype=dtype, device=DEV)
+        dx = torch.full((M, K), float("nan"), dtype=dtype, device=DEV)
+        _lib.call("tt_gmm_fwd", _lib.ptr(x), _lib.ptr(w), *args, _lib.ptr(y), _lib.stream())
+        _lib.call("tt_gmm_dgrad", _lib.ptr(dy), _lib.ptr(w), *args, _lib.ptr(dx), _lib.stream())
+        torch.cuda.synchronize()
+        wf = w.float()
+        s0 = 0
+        for e, c in enumerate(counts.tolist()):
+            we = wf[e].t() if trans_b else wf[e]  # [K, N]
+            assert torch.equal(y[s0:s0 + c], (x[s0:s0 + c].float() @ we).to(dtype)), (rep, e, c)
+            assert torch.equal(dx[s0:s0 + c], (dy[s0:s0 + c].float() @ we.t()).to(dtype)), (rep, e, c)
+            s0 += c
+
+
 # more 256x256 output tiles than the GPU has compute units, so every persistent block
 # walks many tiles (tile switch, cross-tile prefetch, XCD remap); mean expert loads above
 # 512 rows take the four-stage weight-gradient kernel, at most 512 the persistent

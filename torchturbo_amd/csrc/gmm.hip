@@ -93,9 +93,18 @@ __device__ __forceinline__ int xcd_remap(int b, int nb) {
 
 // Block-wide exclusive scans over the E expert counts: row starts and
 // m-tile starts. Writes E + 1 entries of each into LDS.
+// tile_start[e]: prefix of the experts' m-tile counts ceil(rows / BM); with
+// thin_tj > 0 (the persistent fwd / dgrad kernel), of their schedule slots
+// instead: ceil(rows / BM) * thin_tj tiles, or for an expert of at most 64
+// rows ceil(thin_tj / 2) slots of two thin tiles each.
 template <int NT>
 __device__ void scan_counts(const int64_t* __restrict__ counts, int E, int BM,
-                            int64_t* row_start, int* tile_start) {
+                            int64_t* row_start, int* tile_start, int thin_tj = 0) {
+  auto slots = [&](int64_t c) -> int {
+    if (thin_tj == 0) return (int)((c + BM - 1) / BM);
+    if (c > 0 && c <= 64) return (thin_tj + 1) / 2;
+    return (int)((c + BM - 1) / BM) * thin_tj;
+  };
   __shared__ int64_t wrow[NT / 64];
   __shared__ int wtile[NT / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -107,7 +116,7 @@ __device__ void scan_counts(const int64_t* __restrict__ counts, int E, int BM,
     if (e < E) {
       const int64_t c = counts[e];
       r += c;
-      tl += (int)((c + BM - 1) / BM);
+      tl += slots(c);
     }
   }
   int64_t ri = r;
@@ -141,7 +150,7 @@ __device__ void scan_counts(const int64_t* __restrict__ counts, int E, int BM,
       tile_start[e] = tb;
       const int64_t c = counts[e];
       rb += c;
-      tb += (int)((c + BM - 1) / BM);
+      tb += slots(c);
     }
   }
   if (tid == NT - 1) {
@@ -163,6 +172,7 @@ struct TileDesc {
   int64_t i0, j0;   // tile origin
   int64_t seg0, nrows;
   int e;
+  int nsub;  // persistent fwd / dgrad: thin tiles in this slot (0: one ordinary tile)
 };
 
 // Weight-gradient tiles of one block per tile (gmm_mfma_kernel): each
@@ -777,11 +787,12 @@ __device__ __forceinline__ void tile_at(int L, const char* p0, const char* p1, c
                                         int64_t K, int64_t N, int E, int tiles_j,
                                         const int64_t* row_start, const int* tile_start,
                                         TileDesc& t) {
-  const int slot = L / tiles_j, jt = L % tiles_j;
-  // Last e with tile_start[e] <= slot (tile_start is non-decreasing and
-  // tile_start[0] = 0): the wave's 64 lanes test 64 evenly spaced candidates
-  // of the range at once, and the count of lanes that pass narrows the range
-  // to one stride (one LDS round trip per 64-fold narrowing).
+  const int slot = L;
+  // Last e with tile_start[e] <= slot (tile_start, the experts' schedule-slot
+  // prefix, is non-decreasing and tile_start[0] = 0): the wave's 64 lanes
+  // test 64 evenly spaced candidates of the range at once, and the count of
+  // lanes that pass narrows the range to one stride (one LDS round trip per
+  // 64-fold narrowing).
   const int lane = __lane_id();
   int lo = 0, span = E;
   while (span > 1) {
@@ -809,8 +820,16 @@ __device__ __forceinline__ void tile_at(int L, const char* p0, const char* p1, c
     t.I = t.nrows; t.J = K; t.R = N;
     t.c = out + t.seg0 * K * ESZ; t.ldc = K;
   }
-  t.i0 = (int64_t)(slot - ts_e) * DM_BM;
-  t.j0 = (int64_t)jt * DM_BN;
+  const int local = slot - ts_e;
+  if (t.nrows > 0 && t.nrows <= 64) {  // two thin tiles per slot
+    t.i0 = 0;
+    t.j0 = (int64_t)(2 * local) * DM_BN;
+    t.nsub = min(2, tiles_j - 2 * local);
+  } else {
+    t.i0 = (int64_t)(local / tiles_j) * DM_BM;
+    t.j0 = (int64_t)(local % tiles_j) * DM_BN;
+    t.nsub = 0;
+  }
 }
 
 // ===========================================================================
@@ -1057,7 +1076,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   extern __shared__ __align__(16) char smem[];  // expert schedule
   int64_t* row_start = reinterpret_cast<int64_t*>(smem);
   int* tile_start = reinterpret_cast<int*>(row_start + E + 1);
-  scan_counts<DM_NT>(counts, E, DM_BM, row_start, tile_start);
+  scan_counts<DM_NT>(counts, E, DM_BM, row_start, tile_start, WG ? 0 : tiles_j);
 
   const int G = gridDim.x;
   // fwd / dgrad: block position pos walks tiles pos, pos + G, ... (XCD-grouped
@@ -1070,7 +1089,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   int q0 = 0;
   if constexpr (!WG) {
     pos = xcd_remap(blockIdx.x, G);
-    total = tile_start[E] * tiles_j;
+    total = tile_start[E];  // schedule slots
     if (pos >= total) return;
     ntiles = (total - pos + G - 1) / G;
   } else {
@@ -1368,17 +1387,21 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       if (!LAST) frag(mv_c, nxt, 0, i, a0, b0);
   };
 
-  // k-tile 0 whole and the A half of k-tile 1 (its B half goes out in the
-  // first step).
+  // Start of the streamed pipeline (the first tile, and a tile after a thin
+  // one): k-tile 0 whole and the A half of k-tile 1 (its B half goes out in
+  // the first step), then k-step 0's fragments.
+  auto prologue = [&]() {
 #pragma unroll
-  for (int q = 0; q < 16; ++q) issue_one(stage(0), 0, false, q);
+    for (int q = 0; q < 16; ++q) issue_one(stage(0), 0, false, q);
 #pragma unroll
-  for (int q = 0; q < 8; ++q) issue_one(stage(1), 1, false, q);
-  TT_WAIT_VMCNT(8);
-  __builtin_amdgcn_s_barrier();
-  refresh(0);
+    for (int q = 0; q < 8; ++q) issue_one(stage(1), 1, false, q);
+    TT_WAIT_VMCNT(8);
+    __builtin_amdgcn_s_barrier();
+    refresh(0);
 #pragma unroll
-  for (int i = 0; i < FM + FN; ++i) frag(std::integral_constant<int, FM>{}, stage(0), 0, i, a0, b0);
+    for (int i = 0; i < FM + FN; ++i)
+      frag(std::integral_constant<int, FM>{}, stage(0), 0, i, a0, b0);
+  };
 
   lds_char* const epi = (lds_char*)epi_raw + wave * P_EPI;
   // One output tile with MV blocks per wave: its k-tiles, then the epilogue
@@ -1394,7 +1417,105 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     __builtin_amdgcn_sched_barrier(0);
     store_wave_tile_p64<ET, 2, EPI_ROWS, MV>(acc, tc, tc.i0 + a_row0, tc.j0 + wn * WT, epi);
   };
+  // Thin tiles (fwd / dgrad, at most 64 rows: one 32-row block per wave row)
+  // stream a whole weight panel for a quarter of a tile's MFMAs, so the
+  // weight loads in flight set their time. They run a pipeline of their own
+  // with two weight k-tiles in flight while a third is multiplied (one in
+  // the streamed pipeline): the weights in a ring of three 32 KiB slots and
+  // the 64 activation rows in a ring of three 8 KiB slots, both in the stage
+  // memory; one barrier per k-tile, fragment reads one k-step ahead of the
+  // MFMAs. The streamed pipeline stops before such a tile (what it
+  // prefetched for it is discarded) and restarts after it. An expert of at
+  // most 64 rows takes its thin tiles two per schedule slot (each costs
+  // about 0.6 of a full tile), so the static schedule stays balanced.
+  constexpr bool THIN = !WG;
+  constexpr uint32_t THIN_A = 3 * P_OPND;  // activation ring after the weight ring
+  auto thin_tile = [&]() {
+    TT_WAIT_VMCNT(0);  // the previous loads and stores have landed
+    TT_LDS_BARRIER();  // and every wave is past its reads of the stage memory
+    // Activation chunks c = 2 wave, 2 wave + 1 of the tile: rows 8 c + lane / 8.
+    uint32_t tro[2];
+    if constexpr (GA) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int64_t row = tc.i0 + 8 * (2 * wave + p) + (lane >> 3);
+        const int64_t at = tc.seg0 + row;
+        const uint32_t v = (uint32_t)arow[at < M ? at : M - 1];
+        tro[p] = row < tc.nrows ? v * (uint32_t)(lda * 2) : GA_NOROW;
+      }
+    }
+    auto thin_b = [&](int k) {  // weight k-tile k into ring slot k % 3
+      const uint32_t slot = lds_addr_of(lds) + (uint32_t)(k % 3) * P_OPND;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        uint32_t vb = (q & 1) ? vodd[1] : vbase[1];
+        asm volatile("" : "+v"(vb));
+        uint32_t off = vb + ((uint32_t)(q >> 1) * qstep[1] + (uint32_t)k * kstep[1]);
+        if constexpr (KMASK) {
+          if (Lay::B_K && k * P_BK + ((q & 1) ? kof_odd : kof) >= kvalid) off = DM_OOB;
+        }
+        dma16(off, rb_cur, slot + (uint32_t)(8 * wave + q) * 1024u);
+      }
+    };
+    auto thin_a = [&](int k) {  // activation k-tile k (64 rows) into ring slot k % 3
+      const uint32_t slot = lds_addr_of(lds) + THIN_A + (uint32_t)(k % 3) * 8192u;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int c = 2 * wave + p;
+        uint32_t off;
+        if constexpr (GA) {
+          off = tro[p] + (uint32_t)(2 * ((c & 1) ? kof_odd : kof)) + (uint32_t)k * kstep[0];
+        } else {
+          // wave 0's chunk c: this wave's chunk offsets less its 64-row origin
+          off = ((c & 1) ? vodd[0] : vbase[0]) - (uint32_t)(64 * wave * lda * 2) +
+                (uint32_t)(c >> 1) * qstep[0] + (uint32_t)k * kstep[0];
+        }
+        if constexpr (KMASK) {
+          if (k * P_BK + ((c & 1) ? kof_odd : kof) >= kvalid) off = DM_OOB;
+        }
+        dma16(off, ra_cur, slot + (uint32_t)c * 1024u);
+      }
+    };
+    f32x16 acc[FM][FN];  // block row 0 only
+    uint4 ta[2], tb[2][FN];
+    const f32x16 zero = {};
+    auto thin_frags = [&](lds_char* sa, lds_char* sb, int s, int buf) {
+      refresh(s);
+      ta[buf] = read_k(sa, ao);
+#pragma unroll
+      for (int ni = 0; ni < FN; ++ni)
+        tb[buf][ni] = Lay::B_K ? read_k(sb, bo - P_OPND + ni * 4096)
+                               : read_mn(sb, bm[ni] - P_OPND + s * 8192);
+    };
+    thin_a(0);
+    thin_b(0);
+    thin_a(1);
+    thin_b(1);
+    for (int kt = 0; kt < nkt_c; ++kt) {
+      // k-tile kt in (k-tile kt + 1 stays in flight), and every wave is past
+      // k-tile kt - 1, whose slots the loads of k-tile kt + 2 refill.
+      TT_WAIT_VMCNT(10);
+      TT_LDS_BARRIER();
+      thin_a(kt + 2);
+      thin_b(kt + 2);
+      lds_char* const sa = lds + THIN_A + (kt % 3) * 8192;
+      lds_char* const sb = lds + (kt % 3) * P_OPND;
+      thin_frags(sa, sb, 0, 0);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s < 3) thin_frags(sa, sb, s + 1, (s + 1) & 1);
+#pragma unroll
+        for (int ni = 0; ni < FN; ++ni)
+          acc[0][ni] = Mma<ET>::run(tb[s & 1][ni], ta[s & 1],
+                                    (kt == 0 && s == 0) ? zero : acc[0][ni]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    store_wave_tile_p64<ET, 2, EPI_ROWS, 1>(acc, tc, tc.i0 + a_row0, tc.j0 + wn * WT, epi);
+  };
+
   int g = 0;
+  bool pro = true;  // the streamed pipeline has to start (prologue)
   for (;;) {
     // Blocks of 32 rows that hold rows of the expert, per wave row (the
     // interleaved blocks of a tile with b of them: ceil(b / 2)).
@@ -1404,9 +1525,34 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       const int nb32 = left >= DM_BM ? 8 : (int)((left + 31) / 32);
       mv = nb32 <= 2 ? 1 : (nb32 <= 4 ? 2 : 4);
     }
-    if (mv == 4) run_tile(std::integral_constant<int, 4>{}, g);
-    else if (mv == 2) run_tile(std::integral_constant<int, 2>{}, g);
-    else run_tile(std::integral_constant<int, 1>{}, g);
+    if (THIN && mv == 1) {
+      if constexpr (GA) {
+        TT_WAIT_VMCNT(0);
+        gather_offsets(ro_nxt);  // the next tile's rows, loaded at the last switch
+      }
+      const int nsub = tc.nsub > 0 ? tc.nsub : 1;
+      for (int u = 0; u < nsub; ++u) {
+        if (u > 0) {
+          tc.j0 += DM_BN;
+          rb_cur = rsrc_b(tc, true);
+        }
+        thin_tile();
+      }
+      pro = true;
+    } else {
+      if (pro) {
+        // A thin tile's last loads have landed and every wave is past its
+        // reads of the rings before the stages refill.
+        TT_WAIT_VMCNT(0);
+        TT_LDS_BARRIER();
+        g = 0;
+        prologue();
+        pro = false;
+      }
+      if (mv == 4) run_tile(std::integral_constant<int, 4>{}, g);
+      else if (mv == 2) run_tile(std::integral_constant<int, 2>{}, g);
+      else run_tile(std::integral_constant<int, 1>{}, g);
+    }
     if (!has_next) break;
     tc = tn;
     nkt_c = nkt_n;
@@ -1434,10 +1580,12 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     // fragments. A tile with fewer row blocks than the next tile's variant
     // did not read the extra A blocks: read every fragment again when the
     // variants may differ.
-    refresh(0);
+    if (!pro) {
+      refresh(0);
 #pragma unroll
-    for (int i = 0; i < FM + FN; ++i)
-      frag(std::integral_constant<int, FM>{}, stage(g), 0, i, a0, b0);
+      for (int i = 0; i < FM + FN; ++i)
+        frag(std::integral_constant<int, FM>{}, stage(g), 0, i, a0, b0);
+    }
   }
   TT_WAIT_VMCNT(0);  // loads issued past the last tile land before the block exits
 }
