@@ -34,7 +34,10 @@
 //   (the next tile's first loads overlap the current tile's last k-tile and
 //   epilogue); the epilogue stages through a private 4 KiB of LDS per wave
 //   and stores with buffer stores whose resource ends at the expert's last
-//   row.
+//   row. fwd/dgrad tiles of at most 64 rows leave that stream for a
+//   weight-streaming pipeline of their own (two weight k-tiles in flight
+//   while a third is multiplied), and an expert of at most 64 rows takes its
+//   tiles two per schedule slot.
 // * gmm_fp8_kernel (fwd/dgrad with e4m3 weights and 128x128 block scales):
 //   the same tiles and pipeline; the weight tile arrives in LDS as e4m3
 //   bytes and each wave decodes its own rows in hardware, multiplies by the
@@ -44,7 +47,8 @@
 // * gmm_f32_kernel (fp32 operands): 64x64 tiles on fp32 MFMAs
 //   (v_mfma_f32_32x32x2_f32).
 //
-// Tile schedule: fwd/dgrad blocks walk (expert, m-tile, n-tile) slots whose
+// Tile schedule: fwd/dgrad blocks walk (expert, m-tile, n-tile) slots (two
+// n-tiles per slot for an expert of at most 64 rows) whose
 // count is only known on the device; every block derives its slot from the
 // per-expert counts (a block-wide scan in LDS) and blocks past the last slot
 // exit. fwd/dgrad block ids are remapped so that consecutive slots (sharing an
