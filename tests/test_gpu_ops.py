@@ -923,7 +923,7 @@ def _zipf_counts(E, M, seed, empty=(3, 17)):
 # Shapes of the Qwen3-30B-A3B layer's two GEMMs (fc1: K 2048 -> N 1536, fc2: K 768 ->
 # N 2048), tens of thousands of rows, Zipf loads with empty experts. Each launch has far
 @pytest.mark.parametrize("trans_b", [False, True])
-@pytest.mark.parametrize("E,K,N", [(256, 512, 1536), (96, 320, 768), (40, 256, 1000)])
+@pytest.mark.parametrize("E,K,N", [(256, 512, 1536), (96, 320, 768), (40, 256, 1000), (24, 96, 200)])
 def test_grouped_matmul_thin_experts_exact(trans_b, E, K, N):
     """Many experts of at most 64 rows (their output tiles are taken two per schedule
     slot by the persistent fwd / dgrad kernel, an odd number of column tiles leaving
