@@ -669,8 +669,8 @@ def test_permute_unpermute_round_trip_full_qwen_size(hip_ops):
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("with_probs", [False, True])
-def test_swiglu_matches_oracle(hip_ops, dtype, with_probs):
-    rows, F = 333, 96
+@pytest.mark.parametrize("rows,F", [(333, 96), (129, 1000)])  # 1000: an odd count of 16-byte vectors
+def test_swiglu_matches_oracle(hip_ops, dtype, with_probs, rows, F):
     g = torch.Generator().manual_seed(7)
     x = (torch.randn(rows, 2 * F, generator=g) * 2).to(dtype)
     p = torch.rand(rows, generator=g)

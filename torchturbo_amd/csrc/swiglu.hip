@@ -291,11 +291,14 @@ __global__ __launch_bounds__(256) void gated_bwd_kernel(
 bool float_dtype(int d) { return d == TT_F32 || d == TT_BF16 || d == TT_F16; }
 
 // Lanes per row: the power of two <= 64 that wastes the fewest lane slots
-// over the row's vectors (larger on ties).
+// over the row's vectors (larger on ties), and at least 8 once the row has
+// 8 vectors, so that a load covers whole 128-byte lines of a row. (With an
+// odd vector count fewer lanes waste nothing, but one lane per row spreads
+// every load over 64 rows and runs about 30x slower.)
 int lanes_per_row(int64_t nv) {
   int best = 1;
   int64_t best_waste = -1;
-  for (int L = 64; L >= 1; L >>= 1) {
+  for (int L = 64; L >= (nv >= 8 ? 8 : 1); L >>= 1) {
     const int64_t waste = ((nv + L - 1) / L) * L - nv;
     if (best_waste < 0 || waste < best_waste) {
       best = L;
