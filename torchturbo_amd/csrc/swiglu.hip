@@ -72,21 +72,34 @@ __device__ __forceinline__ void sig_silu(float g, float& sig, float& silu) {
 
 constexpr int promote(int a, int b) { return (b == NO_PROBS || a == b) ? a : TT_F32; }
 
-template <class TT, int PD, int V>
+// A row of nv vectors is split into nseg segments of seg vectors (the last
+// shorter), each taken by L lanes: long rows then spread over several waves
+// instead of one wave walking the whole row.
+// SEG: the split launch (nseg > 1); whole rows otherwise.
+template <class TT, int PD, int V, bool SEG>
 __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const typename TT::storage* __restrict__ x,
                                                          int64_t rows, int64_t F,
                                                          const void* __restrict__ probs, int L,
+                                                         int nseg, int64_t seg,
                                                          typename TT::storage* __restrict__ out) {
   typedef typename TT::storage St;
   constexpr int XD = Traits<TT>::code, PR = promote(XD, PD);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
-  if (r >= rows) return;
+  const int64_t vr = ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
+  const int64_t nv = F / V;
+  int64_t r = vr, v0 = 0, v1 = nv;
+  if constexpr (SEG) {
+    if (vr >= rows * nseg) return;
+    r = (int64_t)((uint64_t)vr / (uint32_t)nseg);
+    v0 = (vr - r * nseg) * seg;
+    v1 = v0 + seg < nv ? v0 + seg : nv;
+  } else {
+    if (vr >= rows) return;
+  }
   const float p = load_prob<PD>(probs, r);
   const St* xr = x + r * 2 * F;
   St* orow = out + r * F;
-  const int64_t nv = F / V;
-  for (int64_t v = lane & (L - 1); v < nv; v += L) {
+  for (int64_t v = v0 + (lane & (L - 1)); v < v1; v += L) {
     St g[V], u[V], o[V];
     // Streaming loads (each input element is read once); the output keeps
     // plain stores, which measured faster here than streaming ones.
@@ -290,15 +303,20 @@ __global__ __launch_bounds__(256) void gated_bwd_kernel(
 
 bool float_dtype(int d) { return d == TT_F32 || d == TT_BF16 || d == TT_F16; }
 
-// Lanes per row: the power of two <= 64 that wastes the fewest lane slots
-// over the row's vectors (larger on ties), and at least 8 once the row has
-// 8 vectors, so that a load covers whole 128-byte lines of a row. (With an
-// odd vector count fewer lanes waste nothing, but one lane per row spreads
-// every load over 64 rows and runs about 30x slower.)
+// Lanes per row: the largest power of two <= 64 that leaves at most an
+// eighth of its lane slots idle over the row's vectors; failing that, the
+// one that wastes the fewest (larger on ties), at least 8 once the row has
+// 8 vectors. Fewer lanes per row put more rows, each its own stream of
+// DRAM pages, under one load, and one lane per row (the fewest-waste choice
+// for an odd vector count) spreads every load over 64 rows and runs about
+// 30x slower.
 int lanes_per_row(int64_t nv) {
+  const int lmin = nv >= 8 ? 8 : 1;
+  for (int L = 64; L >= lmin; L >>= 1)
+    if ((((nv + L - 1) / L) * L - nv) * 8 <= nv) return L;
   int best = 1;
   int64_t best_waste = -1;
-  for (int L = 64; L >= (nv >= 8 ? 8 : 1); L >>= 1) {
+  for (int L = 64; L >= lmin; L >>= 1) {
     const int64_t waste = ((nv + L - 1) / L) * L - nv;
     if (best_waste < 0 || waste < best_waste) {
       best = L;
@@ -316,17 +334,35 @@ int launch_fwd_p(const void* x, int64_t rows, int64_t F, const void* probs, void
                        static_cast<uintptr_t>(F * sizeof(St));
   const St* xp = static_cast<const St*>(x);
   St* op = static_cast<St*>(out);
+  // Rows of more than 256 vectors go out in segments of a multiple of 64
+  // vectors, at most 256 (four loads per lane).
+  auto split = [](int64_t nv, int& nseg, int64_t& seg) {
+    nseg = nv > 256 ? (int)((nv + 255) / 256) : 1;
+    seg = nseg > 1 ? (((nv + nseg - 1) / nseg + 63) / 64) * 64 : nv;
+  };
+  int nseg;
+  int64_t seg;
   if (al % 16 == 0) {
     constexpr int V = 16 / sizeof(St);
-    const int L = lanes_per_row(F / V);
-    const int64_t rpb = 4 * (64 / L);
-    hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, V>), dim3((unsigned)((rows + rpb - 1) / rpb)),
-                       dim3(256), 0, s, xp, rows, F, probs, L, op);
+    split(F / V, nseg, seg);
+    const int L = lanes_per_row(seg);
+    const dim3 grid((unsigned)((rows * nseg + 4 * (64 / L) - 1) / (4 * (64 / L))));
+    if (nseg > 1)
+      hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, V, true>), grid, dim3(256), 0, s, xp, rows,
+                         F, probs, L, nseg, seg, op);
+    else
+      hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, V, false>), grid, dim3(256), 0, s, xp, rows,
+                         F, probs, L, nseg, seg, op);
   } else {
-    const int L = lanes_per_row(F);
-    const int64_t rpb = 4 * (64 / L);
-    hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, 1>), dim3((unsigned)((rows + rpb - 1) / rpb)),
-                       dim3(256), 0, s, xp, rows, F, probs, L, op);
+    split(F, nseg, seg);
+    const int L = lanes_per_row(seg);
+    const dim3 grid((unsigned)((rows * nseg + 4 * (64 / L) - 1) / (4 * (64 / L))));
+    if (nseg > 1)
+      hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, 1, true>), grid, dim3(256), 0, s, xp, rows,
+                         F, probs, L, nseg, seg, op);
+    else
+      hipLaunchKernelGGL((swiglu_fwd_kernel<TT, PD, 1, false>), grid, dim3(256), 0, s, xp, rows,
+                         F, probs, L, nseg, seg, op);
   }
   return tt_check_launch("swiglu_fwd");
 }
