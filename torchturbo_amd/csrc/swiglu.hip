@@ -117,15 +117,19 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const typename TT::stor
   }
 }
 
-template <class TT, int PD, int V, bool GP>
+// SEG: one block per row, wave w taking vectors [w seg, (w + 1) seg) with all
+// 64 lanes (L = 64), the four waves' probability-gradient partials summed
+// in wave order; whole rows per lane group otherwise.
+template <class TT, int PD, int V, bool GP, bool SEG>
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     const typename TT::storage* __restrict__ x, int64_t rows, int64_t F,
-    const void* __restrict__ probs, int L, const typename TT::storage* __restrict__ gout,
-    typename TT::storage* __restrict__ gx, void* __restrict__ gprobs) {
+    const void* __restrict__ probs, int L, int64_t seg,
+    const typename TT::storage* __restrict__ gout, typename TT::storage* __restrict__ gx,
+    void* __restrict__ gprobs) {
   typedef typename TT::storage St;
   constexpr int XD = Traits<TT>::code, PR = promote(XD, PD);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t r = ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
+  const int64_t r = SEG ? (int64_t)blockIdx.x : ((int64_t)blockIdx.x * 4 + wave) * (64 / L) + lane / L;
   const bool live = r < rows;  // idle lanes still join the row reduction
   const float p = live ? load_prob<PD>(probs, r) : 0.f;
   float dp = 0.f;
@@ -133,7 +137,9 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   const St* xr = x + r * 2 * F;
   const St* gr = gout + r * F;
   St* dxr = gx + r * 2 * F;
-  for (int64_t v = lane & (L - 1); v < nv; v += L) {
+  const int64_t v0 = SEG ? wave * seg : 0;
+  const int64_t v1 = SEG ? (v0 + seg < nv ? v0 + seg : nv) : nv;
+  for (int64_t v = v0 + (lane & (L - 1)); v < v1; v += L) {
     St g[V], u[V], d[V], og[V], ou[V];
     // Streaming loads and stores: every element is touched once.
     load_stream<sizeof(g)>(g, xr + v * V);
@@ -163,7 +169,15 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   }
   if constexpr (GP) {
     for (int off = L / 2; off > 0; off >>= 1) dp += __shfl_xor(dp, off, TT_WAVE);
-    if (live && (lane & (L - 1)) == 0) store_prob<PD>(gprobs, r, dp);
+    if constexpr (SEG) {
+      __shared__ float part[4];
+      if (lane == 0) part[wave] = dp;
+      __syncthreads();
+      if (threadIdx.x == 0 && live)
+        store_prob<PD>(gprobs, r, ((part[0] + part[1]) + part[2]) + part[3]);
+    } else {
+      if (live && (lane & (L - 1)) == 0) store_prob<PD>(gprobs, r, dp);
+    }
   }
 }
 
@@ -376,19 +390,28 @@ int launch_bwd_p(const void* x, int64_t rows, int64_t F, const void* probs, cons
   const St* xp = static_cast<const St*>(x);
   const St* gp = static_cast<const St*>(gout);
   St* dxp = static_cast<St*>(gx);
+  // Rows of more than 256 vectors: one block per row, four segments of a
+  // multiple of 64 vectors.
   if (al % 16 == 0) {
     constexpr int V = 16 / sizeof(St);
-    const int L = lanes_per_row(F / V);
-    const int64_t rpb = 4 * (64 / L);
-    hipLaunchKernelGGL((swiglu_bwd_kernel<TT, PD, V, GP>),
-                       dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, xp, rows, F,
-                       probs, L, gp, dxp, gprobs);
+    const int64_t nv = F / V;
+    if (nv > 256) {
+      const int64_t seg = (((nv + 3) / 4 + 63) / 64) * 64;
+      hipLaunchKernelGGL((swiglu_bwd_kernel<TT, PD, V, GP, true>), dim3((unsigned)rows),
+                         dim3(256), 0, s, xp, rows, F, probs, 64, seg, gp, dxp, gprobs);
+    } else {
+      const int L = lanes_per_row(nv);
+      const int64_t rpb = 4 * (64 / L);
+      hipLaunchKernelGGL((swiglu_bwd_kernel<TT, PD, V, GP, false>),
+                         dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, xp, rows, F,
+                         probs, L, nv, gp, dxp, gprobs);
+    }
   } else {
     const int L = lanes_per_row(F);
     const int64_t rpb = 4 * (64 / L);
-    hipLaunchKernelGGL((swiglu_bwd_kernel<TT, PD, 1, GP>),
+    hipLaunchKernelGGL((swiglu_bwd_kernel<TT, PD, 1, GP, false>),
                        dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, s, xp, rows, F,
-                       probs, L, gp, dxp, gprobs);
+                       probs, L, F, gp, dxp, gprobs);
   }
   return tt_check_launch("swiglu_bwd");
 }
