@@ -7,7 +7,7 @@ synthetic inputs already resident in HBM (``MoELayer.forward_with_logits``
 with every op served by the HIP providers). On one GPU the layer folds the
 permutation into fc1 and the unpermutation's backward into fc2's gradients
 (the GEMMs gather token rows through the routing index), when the shapes
-allow: the Qwen, Mixtral and varlen layers. Default workload: the
+allow: the Qwen and varlen layers (Mixtral stays packed). Default workload: the
 Qwen3-30B-A3B-shaped layer (16384 tokens, hidden 2048, 128 experts, top-8,
 ffn 768, bf16, Zipf-skewed fp32 router logits).
 

@@ -9,12 +9,15 @@ cannot run the whole layer in seconds, but it does not need to:
   experts it is routed to. ``token_rows`` runs the oracle on a token subset
   with only the experts that subset uses (experts renumbered in order, which
   keeps the expert-major packed order);
-* the weight gradient of expert e depends only on the tokens routed to e, and
-  the gate / up columns c of dW1[e] and the rows c of dW2[e] only on the ffn
-  columns c of every expert (SwiGLU is elementwise, and the unweighted
-  combine's backward does not depend on the forward values). ``expert_grads``
-  runs the oracle on every token routed to the chosen experts, on an ffn
-  column slice, and returns those experts' gradients on that slice.
+* the weight gradient of expert e depends only on the tokens routed to e and
+  on expert e's own term of the layer sum (the output gradient is given, and
+  the unweighted combine passes each packed row its token's gradient row),
+  and the gate / up columns c of dW1[e] and the rows c of dW2[e] only on the
+  ffn columns c (SwiGLU is elementwise). ``expert_grads`` runs the oracle's
+  expert terms (grouped matmul, SwiGLU x probability, grouped matmul) of the
+  chosen experts on every token routed to them, on an ffn column slice, and
+  returns those experts' gradients on that slice; no other expert is
+  evaluated, so the most-loaded expert of a full-size layer stays cheap.
 
 Both results equal the rows / slices of the full oracle run up to the
 summation order of CPU matrix products (``test_sampled_oracle_matches_full``).
@@ -130,14 +133,43 @@ def expert_grads(hidden, logits, grad, cfg, bias, weights: ExpertWeights, expert
     equal), used to find every token routed to the chosen experts."""
     if full_ids is None:
         full_ids = o_layer.route(logits, cfg, bias)[2]
-    chosen = torch.zeros(logits.shape[1], dtype=torch.bool)
-    chosen[torch.as_tensor(experts)] = True
-    tokens = chosen[full_ids].any(dim=1).nonzero().flatten()
-    res = _run(hidden, logits, grad, cfg, bias, weights, tokens, f_slice, None)
-    keep = {int(e) for e in experts}
-    res.d_w1 = {e: g for e, g in res.d_w1.items() if e in keep}
-    res.d_w2 = {e: g for e, g in res.d_w2.items() if e in keep}
-    return res
+    E = logits.shape[1]
+    chosen = sorted({int(e) for e in experts})
+    mask = torch.zeros(E, dtype=torch.bool)
+    mask[chosen] = True
+    tokens = mask[full_ids].any(dim=1).nonzero().flatten()
+    probs, rmap, _ = o_layer.route(logits[tokens], cfg, bias)
+    # Packed rows of the chosen experts: experts ascending, tokens ascending
+    # (the permutation's order restricted to these experts).
+    sub = rmap[:, chosen]
+    counts = sub.sum(dim=0).long()
+    cell = sub.t().contiguous().reshape(-1).nonzero().flatten()
+    row_token = cell % max(tokens.numel(), 1)
+    row_expert = cell // max(tokens.numel(), 1)
+    x = hidden[tokens][row_token]
+    p = probs[:, chosen].t().reshape(-1)[cell]
+    g_rows = grad[tokens][row_token]
+    sel = weights.select(torch.tensor(chosen), f_slice)
+    if sel.fp8:
+        m1 = dequantize_experts(sel.q1, sel.s1).requires_grad_()
+        m2 = dequantize_experts(sel.q2, sel.s2).requires_grad_()
+        fc1 = o_layer.grouped_matmul_fp8(x, sel.q1, sel.s1, counts, master=m1, stacked_grad=True)
+        act = o_layer.swiglu_probs(fc1, p)
+        fc2 = o_layer.grouped_matmul_fp8(act, sel.q2, sel.s2, counts, master=m2,
+                                         stacked_grad=True)
+        g1, g2 = m1, m2
+    else:
+        g1 = sel.w1.detach().requires_grad_()  # shares storage; nothing writes it
+        g2 = sel.w2.detach().requires_grad_()
+        fc1 = o_layer.grouped_matmul(x, g1, counts, stacked_grad=True)
+        act = o_layer.swiglu_probs(fc1, p)
+        fc2 = o_layer.grouped_matmul(act, g2, counts, stacked_grad=True)
+    fc2.backward(g_rows.to(fc2.dtype))
+    assert torch.equal(row_expert.bincount(minlength=len(chosen)), counts)
+    d_w1 = {e: g1.grad[i] for i, e in enumerate(chosen)}
+    d_w2 = {e: g2.grad[i] for i, e in enumerate(chosen)}
+    empty = torch.empty(0)
+    return SampleResult(tokens, empty, empty, empty, full_ids[tokens], d_w1, d_w2)
 
 
 __all__ = ["ExpertWeights", "SampleResult", "expert_grads", "token_rows"]

@@ -1112,12 +1112,17 @@ def test_grouped_matmul_fp8_many_tiles(hip_ops):
     deq = o_fp8.dequantize_experts(q, s).to(DEV)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV).requires_grad_()
     dy = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
-    y = hip_ops.grouped_matmul_fp8(x, q.to(DEV), s.to(DEV), counts)
+    mw = deq.clone().requires_grad_()  # bf16 master weights [E, N, K]
+    y = hip_ops.grouped_matmul_fp8(x, q.to(DEV), s.to(DEV), counts, master=mw)
     y.backward(dy)
     xs = torch.split(x.detach().float(), counts)
     ds = torch.split(dy.float(), counts)
     yr = torch.cat([xs[e] @ deq[e].float().t() for e in range(E)])
     dxr = torch.cat([ds[e] @ deq[e].float() for e in range(E)])
-    for a, b, name in ((y, yr, "y"), (x.grad, dxr, "dx")):
+    # master-weight gradient dW[e] = dy_e^T @ x_e ([N, K]); empty experts exactly zero
+    dwr = torch.stack([ds[e].t() @ xs[e] for e in range(E)])
+    for a, b, name in ((y, yr, "y"), (x.grad, dxr, "dx"), (mw.grad, dwr, "d_master")):
         mx, mean = rel_errors(a.float().cpu(), b.cpu())
         assert mx <= 1e-2 and mean <= 2e-3, f"{name}: {mx:.3e} {mean:.3e}"
+    for e in (3, 17):
+        assert torch.count_nonzero(mw.grad[e]) == 0, e

@@ -88,3 +88,62 @@ def test_sampled_oracle_matches_full(fp8):
             full2 = g2.grad[e, c0:c1]
         _close(res.d_w1[e], full1, fp32, f"d_w1[{e}]")
         _close(res.d_w2[e], full2, fp32, f"d_w2[{e}]")
+
+
+def _fp32_full_run():
+    w = replace(C.QWEN3, tokens=192, hidden=128, ffn=96, experts=16, topk=4, dtype=torch.float32)
+    hidden, logits, grad = C.make_hidden(w), C.make_logits(w), C.make_grad(w)
+    bias = C.make_expert_bias(w)
+    m1, m2 = C.make_weights(w)
+    cfg = _cfg(w)
+    w1r, w2r = m1.clone().requires_grad_(), m2.clone().requires_grad_()
+    hr, lr = hidden.clone().requires_grad_(), logits.clone().requires_grad_()
+    out, trace = o_layer.moe_layer(hr, lr, w1r, w2r, cfg, expert_bias=bias, trace=True)
+    out.backward(grad)
+    return w, (hidden, logits, grad, cfg, bias), (m1, m2), out.detach(), hr.grad, w1r.grad, trace
+
+
+def _planted(m1, m2, mistake):
+    """ExpertWeights whose ``select`` makes one slicing / renumbering mistake."""
+    def getter(experts, f_slice):
+        sel = ExpertWeights(w1=m1, w2=m2).select(experts, f_slice)
+        if mistake == "swap_experts":  # renumbering: the first two selected experts trade weights
+            order = torch.arange(experts.numel())
+            order[[0, 1]] = order[[1, 0]]
+            return ExpertWeights(w1=sel.w1[order].contiguous(), w2=sel.w2[order].contiguous())
+        c0, c1 = f_slice  # up_from_gate: the up half of the slice is the gate's columns
+        gate = m1[experts][:, :, c0:c1]
+        return ExpertWeights(w1=torch.cat([gate, gate], dim=2).contiguous(), w2=sel.w2)
+
+    return ExpertWeights(w1=m1, w2=m2, getter=getter)
+
+
+@pytest.mark.parametrize("mistake", ["up_from_gate", "swap_experts"])
+def test_sampled_oracle_planted_mistake_fails(mistake):
+    """A slicing mistake (up columns taken from the gate half) or a renumbering
+    mistake (two experts' weights swapped) in the sampled oracle makes its
+    result differ from the full run well beyond the fp32 bound the GPU-side
+    comparison relies on, so the decomposition check above would catch it."""
+    w, inputs, (m1, m2), out, d_hidden, d_w1, trace = _fp32_full_run()
+    hidden, logits, grad, cfg, bias = inputs
+    bad = _planted(m1, m2, mistake)
+    if mistake == "swap_experts":
+        tokens = torch.arange(0, 192, 7)
+        rows = token_rows(hidden, logits, grad, cfg, bias, bad, tokens)
+        mx, _ = rel_errors(rows.out, out[tokens])
+        assert mx > 1e-2, mx
+        # the same call with the correct weights agrees
+        good = token_rows(hidden, logits, grad, cfg, bias, ExpertWeights(w1=m1, w2=m2), tokens)
+        assert rel_errors(good.out, out[tokens])[0] <= 1e-5
+    else:
+        counts = trace.tokens_per_expert
+        e = int(torch.argsort(counts)[-1])
+        c0, c1 = 32, 64
+        Fd = w.ffn
+        res = expert_grads(hidden, logits, grad, cfg, bias, bad, [e], f_slice=(c0, c1))
+        full1 = torch.cat([d_w1[e, :, c0:c1], d_w1[e, :, Fd + c0:Fd + c1]], dim=1)
+        mx, _ = rel_errors(res.d_w1[e], full1)
+        assert mx > 1e-2, mx
+        good = expert_grads(hidden, logits, grad, cfg, bias, ExpertWeights(w1=m1, w2=m2), [e],
+                            f_slice=(c0, c1))
+        assert rel_errors(good.d_w1[e], full1)[0] <= 1e-5

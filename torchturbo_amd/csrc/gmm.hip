@@ -38,12 +38,20 @@
 //   weight-streaming pipeline of their own (two weight k-tiles in flight
 //   while a third is multiplied), and an expert of at most 64 rows takes its
 //   tiles two per schedule slot.
-// * gmm_fp8_kernel (fwd/dgrad with e4m3 weights and 128x128 block scales):
-//   the same tiles and pipeline; the weight tile arrives in LDS as e4m3
-//   bytes and each wave decodes its own rows in hardware, multiplies by the
-//   block scale and rounds to bf16 (exactly bf16(f32(q) * f32(scale))) into
-//   one of three rotating bf16 tiles, overlapped with the previous k-tile's
-//   MFMAs.
+// * gmm_q8_kernel (fwd/dgrad with e4m3 weights and 128x128 block scales,
+//   every launch whose reduction is longer than one 64-deep k-tile):
+//   persistent like gmm_p64_kernel, 128x512x64 tiles (the four waves share
+//   the tile's 128 rows and take 128 columns each, so an expert's rows are
+//   padded to 128 only). The weight tile stays e4m3 in LDS; each wave reads
+//   its own fragments as e4m3 bytes (plain 8-byte reads of K-major rows in
+//   fwd, the transposing 8-bit read ds_read_b64_tr_b8 of N-major rows in
+//   dgrad) and dequantises them in registers between its MFMAs, exactly
+//   bf16(f32(q) * f32(scale)) with one scale per wave and k-tile.
+// * gmm_fp8_kernel (FP8 fwd/dgrad with a reduction of one k-tile): the
+//   256x256x32 tiles of gmm_mfma_kernel; the weight tile arrives in LDS as
+//   e4m3 bytes and each wave decodes its own rows in hardware, multiplies by
+//   the block scale and rounds to bf16 into one of three rotating bf16
+//   tiles, overlapped with the previous k-tile's MFMAs.
 // * gmm_f32_kernel (fp32 operands): 64x64 tiles on fp32 MFMAs
 //   (v_mfma_f32_32x32x2_f32).
 //

@@ -32,6 +32,11 @@ import torch.distributed as dist
 from ..dispatch import ops
 from .moe_config import MoEConfig
 
+# Sizes the HIP router kernels cover (tt_router_topk_fwd / _bwd,
+# tt_router_loss_fwd: E <= 1024, k <= 64).
+MAX_EXPERTS = 1024
+MAX_TOPK = 64
+
 
 def _op_resolves(name: str) -> bool:
     """Whether the process dispatcher has an implementation of ``name`` for its device."""
@@ -157,6 +162,18 @@ class Router(torch.nn.Module):
 class TopKRouter(Router):
     def __init__(self, config: MoEConfig, layer_number: Optional[int] = None, sp_group=None):
         super().__init__(config=config)
+        # Limits of the HIP top-k kernels (one wave per token, up to 16 experts
+        # per lane, a k-round selection), stated here so that a layer the GPU
+        # cannot route fails when it is built, not on its first call.
+        if config.num_moe_experts > MAX_EXPERTS:
+            raise ValueError(f"TopKRouter: num_moe_experts={config.num_moe_experts} exceeds the "
+                             f"{MAX_EXPERTS} experts the router kernels support")
+        if config.moe_router_topk > MAX_TOPK:
+            raise ValueError(f"TopKRouter: moe_router_topk={config.moe_router_topk} exceeds the "
+                             f"{MAX_TOPK} the router kernels support")
+        if config.moe_router_dtype == "fp64":
+            raise ValueError("TopKRouter: moe_router_dtype='fp64' is not supported by the router "
+                             "kernels (fp32 or the input dtype)")
         self.topk = config.moe_router_topk
         self.routing_type = config.moe_router_load_balancing_type
         self.score_function = config.moe_router_score_function
