@@ -23,7 +23,7 @@ extern "C" {
 #endif
 
 /* dtypes */
-enum { TT_F32 = 0, TT_BF16 = 1, TT_F16 = 2, TT_F8E4M3 = 3 };
+enum { TT_F32 = 0, TT_BF16 = 1, TT_F16 = 2, TT_F8E4M3 = 3, TT_F64 = 4 };
 /* status codes */
 enum { TT_OK = 0, TT_ERR_INVALID = -1, TT_ERR_UNSUPPORTED = -2, TT_ERR_HIP = -3 };
 /* router score functions */
@@ -38,9 +38,13 @@ const char* tt_last_error(void);
  * Replaces topk_softmax_with_capacity / group_limited_topk
  * (models/modules/moe/utils.py:30-80,127-230), called from
  * TopKRouter.routing (models/modules/moe/router.py:277-356).
- * logits [T, E] (f32/bf16/f16) -> probs [T, E] (logits dtype, zeros except
- * the k selected), routing_map [T, E] (bytes 0/1), top_indices [T, k] int64
- * in descending-score order (ties: lower expert id first).
+ * logits [T, E] (f32/bf16/f16/f64) -> probs [T, E] (logits dtype, zeros
+ * except the k selected), routing_map [T, E] (bytes 0/1), top_indices [T, k]
+ * int64 in descending-score order (ties: lower expert id first). With f64
+ * logits (moe_router_dtype "fp64", router.py:97-100) the top-k of the plain
+ * softmax selects on the f64 logits, and the scores, softmax and
+ * renormalisation run in fp32 and are widened, as utils.py:181-224 does
+ * (softmax(..., dtype=float32), logits.float(), probs.type_as(logits)).
  * expert_bias [E] f32 or NULL (selection only). num_groups/group_topk = 0
  * disable group-limited selection. scaling_factor = 0 means none.
  * fixed_indices [T, k] int64 or NULL: hash routing (ids given).
@@ -87,7 +91,8 @@ int tt_router_gate_fwd(const void* x, const void* weight, int in_dtype, int64_t 
  *     first, lower expert id on equal scores);
  *   z_sum [1] f32 = sum_t r(logsumexp(logits_t)^2), r = rounding to the
  *     logits dtype, logsumexp formed in that dtype step by step as
- *     torch.logsumexp does (max, x - max, exp, sum, log, + max).
+ *     torch.logsumexp does (max, x - max, exp, sum, log, + max); for f64
+ *     logits in fp32 (the reference's fp64 logsumexp to fp32 precision).
  * prob_sum and tokens_per_expert are both NULL (aux off) or both set; z_sum
  * may be NULL (z off). Sums are reproducible (fixed grid, fixed order).
  * Workspace: tt_router_loss_workspace(T, E) bytes. E <= 1024. */

@@ -54,6 +54,11 @@ ROUTER_CASES = [
     (77, 16, 1, "softmax", False, None, None, None, False, torch.float32),
     (77, 16, 1, "sigmoid", False, None, None, None, False, torch.float32),
     (500, 128, 8, "softmax", False, None, None, None, False, torch.bfloat16),
+    # fp64 logits (moe_router_dtype "fp64"): selection on the fp64 values
+    (1000, 128, 8, "softmax", False, None, None, None, False, torch.float64),
+    (300, 128, 8, "softmax", True, None, None, 2.0, True, torch.float64),
+    (200, 256, 8, "sigmoid", False, 8, 4, 2.5, True, torch.float64),
+    (64, 512, 8, "softmax", False, 8, 4, None, False, torch.float64),
 ]
 
 
@@ -70,8 +75,9 @@ def test_router_matches_oracle(hip_ops, case):
     dev_logits = logits.to(DEV).requires_grad_()
     probs, rmap, ids = hip_ops.topk_softmax_with_capacity(
         dev_logits, k, **{**kwargs, "expert_bias": None if bias is None else bias.to(DEV)})
-    if dtype == torch.float32:
-        # Bit-exact selection (no ties with fp32 N(0, 1) logits).
+    exact = dtype in (torch.float32, torch.float64)
+    if exact:
+        # Bit-exact selection (no ties with fp32 / fp64 N(0, 1) logits).
         assert torch.equal(ids.cpu(), ids_r)
         assert torch.equal(rmap.cpu(), map_r)
     else:
@@ -82,20 +88,45 @@ def test_router_matches_oracle(hip_ops, case):
         assert torch.equal(rmap.cpu()[clean], map_r[clean])
         assert torch.equal(ids.cpu()[clean].sort(1).values, ids_r[clean].sort(1).values)
     assert probs.dtype == dtype
-    tol = 2e-6 if dtype == torch.float32 else 8e-3
-    rows = slice(None) if dtype == torch.float32 else clean
+    # fp64 logits: the reference forms the probabilities in fp32 and widens them
+    # (softmax(..., dtype=float32), logits.float()), so fp32 rounding is the bar.
+    tol = 2e-6 if exact else 8e-3
+    rows = slice(None) if exact else clean
     mx, _ = rel_errors(probs.cpu()[rows], probs_r[rows])
     assert mx <= tol, mx
     # backward through the dense probs
     w = torch.randn(T, E, generator=g).to(dtype)
     (probs_r * w).sum().backward()
     (probs * w.to(DEV)).sum().backward()
-    if dtype == torch.float32:
+    if exact:
+        assert dev_logits.grad.dtype == dtype
         mx, mean = rel_errors(dev_logits.grad.cpu(), ref_logits.grad)
         assert mx <= 1e-5 and mean <= 1e-6, (mx, mean)
     else:
         clean_rows = clean
         assert_bf16_close(dev_logits.grad.cpu()[clean_rows], ref_logits.grad[clean_rows], what="dlogits")
+
+
+def test_router_fp64_selects_on_fp64_logits(hip_ops):
+    """fp64 logits that differ below fp32 resolution: the reference's top-k of
+    the fp64 logits (utils.py:190-196) orders them by their fp64 values, where
+    fp32 keys would tie and go to the lower expert id."""
+    T, E, k = 64, 32, 2
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(T, E, generator=g, dtype=torch.float64) - 4.0
+    base = torch.rand(T, generator=g, dtype=torch.float64) + 1.0
+    lo = torch.randint(0, E // 2, (T,), generator=g)
+    hi = lo + E // 2
+    logits[torch.arange(T), lo] = base
+    logits[torch.arange(T), hi] = base + 1e-12  # the same fp32 value, larger in fp64
+    assert torch.equal(logits[torch.arange(T), lo].float(), logits[torch.arange(T), hi].float())
+    probs_r, map_r, ids_r = o_route.topk_softmax_with_capacity(logits, k)
+    assert torch.equal(ids_r[:, 0], hi) and torch.equal(ids_r[:, 1], lo)
+    probs, rmap, ids = hip_ops.topk_softmax_with_capacity(logits.to(DEV), k)
+    assert torch.equal(ids.cpu(), ids_r)
+    assert torch.equal(rmap.cpu(), map_r)
+    assert probs.dtype == torch.float64
+    assert rel_errors(probs.cpu(), probs_r)[0] <= 2e-6
 
 
 def test_router_hash_routing(hip_ops):
@@ -248,6 +279,8 @@ LOSS_CASES = [
     (700, 64, 4, "sigmoid", torch.float16, True),
     (5, 1024, 1, "sigmoid", torch.float32, False),
     (0, 16, 2, "softmax", torch.float32, False),
+    (1000, 128, 8, "softmax", torch.float64, False),
+    (777, 33, 3, "sigmoid", torch.float64, True),
 ]
 
 
@@ -267,7 +300,8 @@ def test_router_loss_stats_matches_oracle(hip_ops, case):
     assert ps.dtype == torch.float32 and cn.dtype == torch.int64 and zs.dim() == 0
     n_valid = T - (int(pad.sum()) if pad is not None else 0)
     assert int(cn.sum()) == k * n_valid
-    if dtype == torch.float32:
+    wide = dtype in (torch.float32, torch.float64)
+    if wide:
         assert torch.equal(cn.cpu(), cn_r)
     else:
         # bf16 logits tie; only rows with a tie at the k-th score may differ
@@ -275,8 +309,9 @@ def test_router_loss_stats_matches_oracle(hip_ops, case):
         ties = int((s[:, k - 1] == s[:, k]).sum())
         assert int((cn.cpu() - cn_r).abs().sum()) <= 2 * ties
     torch.testing.assert_close(ps.cpu(), ps_r, rtol=1e-5, atol=1e-5)
-    ztol = 1e-5 if dtype == torch.float32 else 2e-3
-    torch.testing.assert_close(zs.cpu(), zs_r, rtol=ztol, atol=1e-5)
+    # fp64 logits: the reference's fp64 logsumexp, here formed in fp32
+    ztol = 1e-5 if wide else 2e-3
+    torch.testing.assert_close(zs.cpu().to(zs_r.dtype), zs_r, rtol=ztol, atol=1e-5)
     gp = torch.randn(E, generator=g)
     gz = torch.randn((), generator=g)
     ((ps_r * gp).sum() + zs_r * gz).backward()
@@ -286,7 +321,8 @@ def test_router_loss_stats_matches_oracle(hip_ops, case):
         return
     if pad is not None:
         assert not dev.grad.cpu()[pad].any()
-    if dtype == torch.float32:
+    if wide:
+        assert dev.grad.dtype == dtype
         mx, mean = rel_errors(dev.grad.cpu(), ref.grad)
         assert mx <= 2e-5 and mean <= 2e-6, (mx, mean)
     else:
@@ -322,9 +358,11 @@ def test_router_loss_stats_is_reproducible(hip_ops):
         assert torch.equal(x, y)
 
 
-def test_router_aux_and_z_losses_on_gpu_match_cpu(process_ops, monkeypatch):
+@pytest.mark.parametrize("router_dtype", ["fp32", "fp64"])
+def test_router_aux_and_z_losses_on_gpu_match_cpu(process_ops, monkeypatch, router_dtype):
     """TopKRouter with both losses (router.py:164-356) through the HIP ops vs the
-    same router on the CPU oracle: probs, loss metrics, weight and input grads."""
+    same router on the CPU oracle: probs, loss metrics, weight and input grads;
+    fp32 and fp64 router dtypes (router.py:97-100)."""
     from torchturbo_amd.moe import MoEConfig, TopKRouter
     from torchturbo_amd.moe.router import MoEAuxLossAutoScaler
     from torchturbo_amd.runtime import CpuRuntime, CudaRuntime
@@ -334,8 +372,8 @@ def test_router_aux_and_z_losses_on_gpu_match_cpu(process_ops, monkeypatch):
     # the rounding difference of the CPU and GPU fp32 gating GEMMs
     torch.manual_seed(4)
     cfg = MoEConfig(hidden_size=64, num_moe_experts=128, moe_router_topk=8,
-                    moe_router_dtype="fp32", moe_aux_loss_coeff=0.01, moe_z_loss_coeff=0.001,
-                    params_dtype=torch.float32)
+                    moe_router_dtype=router_dtype, moe_aux_loss_coeff=0.01,
+                    moe_z_loss_coeff=0.001, params_dtype=torch.float32)
     router = TopKRouter(cfg)
     torch.nn.init.normal_(router.weight, std=0.2)
     x = torch.randn(4, 128, 64)

@@ -14,7 +14,7 @@ import torch
 
 from .build import library_path
 
-TT_F32, TT_BF16, TT_F16, TT_F8E4M3 = 0, 1, 2, 3
+TT_F32, TT_BF16, TT_F16, TT_F8E4M3, TT_F64 = 0, 1, 2, 3, 4
 TT_SCORE = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 
 _DTYPES = {
@@ -22,6 +22,7 @@ _DTYPES = {
     torch.bfloat16: TT_BF16,
     torch.float16: TT_F16,
     torch.float8_e4m3fn: TT_F8E4M3,
+    torch.float64: TT_F64,
 }
 
 P = c_void_p

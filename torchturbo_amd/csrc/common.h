@@ -36,11 +36,13 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return h;
 }
 
-// Load element i of a tensor of runtime dtype as fp32.
+// Load element i of a tensor of runtime dtype as fp32 (fp64 rounds to
+// nearest, as a cast to fp32 does).
 __device__ __forceinline__ float load_as_f32(const void* p, int dtype, int64_t i) {
   switch (dtype) {
     case TT_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
     case TT_F16: return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case TT_F64: return (float)static_cast<const double*>(p)[i];
     default: return static_cast<const float*>(p)[i];
   }
 }
@@ -58,6 +60,7 @@ __device__ __forceinline__ void store_from_f32(void* p, int dtype, int64_t i, fl
   switch (dtype) {
     case TT_BF16: static_cast<uint16_t*>(p)[i] = f32_to_bf16(v); break;
     case TT_F16: static_cast<uint16_t*>(p)[i] = f32_to_f16(v); break;
+    case TT_F64: static_cast<double*>(p)[i] = (double)v; break;
     default: static_cast<float*>(p)[i] = v; break;
   }
 }
@@ -87,6 +90,7 @@ static inline int tt_promote(int a, int b) {
 
 static inline int tt_elem_size(int dtype) {
   switch (dtype) {
+    case TT_F64: return 8;
     case TT_F32: return 4;
     case TT_BF16: case TT_F16: return 2;
     case TT_F8E4M3: return 1;

@@ -15,6 +15,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -22,21 +23,26 @@ namespace {
 
 constexpr int kRouterWaves = 4;  // tokens per 256-thread block
 
+// KT: the type selection keys are compared in: fp32, or fp64 for fp64
+// logits (whose plain-softmax top-k compares the fp64 logits themselves).
+template <typename KT>
 struct Cand {
-  float sel;   // selection key (score, or score + bias)
+  KT sel;      // selection key (score, or score + bias)
   int idx;     // expert id
   float sc;    // score the probability is computed from
   float lg;    // logit (fp32)
 };
 
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+template <typename KT>
+__device__ __forceinline__ bool better(KT v, int i, KT bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
 // Wave-wide arg-max (segment of `width` lanes when width < 64).
-__device__ __forceinline__ Cand cand_reduce(Cand c, int width) {
+template <typename KT>
+__device__ __forceinline__ Cand<KT> cand_reduce(Cand<KT> c, int width) {
   for (int off = width >> 1; off > 0; off >>= 1) {
-    Cand o;
+    Cand<KT> o;
     o.sel = __shfl_xor(c.sel, off, TT_WAVE);
     o.idx = __shfl_xor(c.idx, off, TT_WAVE);
     o.sc = __shfl_xor(c.sc, off, TT_WAVE);
@@ -61,6 +67,15 @@ __device__ __forceinline__ float wave_max_uniform(float v) {
   v = TT_DPP_FMAX(v, 0x143, 0xc);  // row_bcast31 into rows 2 and 3
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// The same for fp64 keys: a butterfly of shuffles, then lane 0's value.
+__device__ __forceinline__ double wave_max_uniform(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmax(v, __shfl_xor(v, off, TT_WAVE));
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readfirstlane((int)b);
+  const int hi = __builtin_amdgcn_readfirstlane((int)(b >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
@@ -72,14 +87,18 @@ __device__ __forceinline__ float softplus_f(float x) {
 // Top-k routing of token t by one wave from its logits (fp32 values of the
 // logits dtype ldt; lane l holds experts l*EPL .. l*EPL + EPL - 1, -inf past
 // E): scores, selection, probabilities, and the outputs of row t.
-template <int EPL>
+// kl: the logits as selection keys (the fp64 logits for KT = double, lg
+// otherwise).
+template <int EPL, typename KT = float>
 __device__ __forceinline__ void route_row(
-    int lane, int64_t t, const float (&lg)[EPL], const bool (&valid)[EPL], int ldt, int E, int K,
-    int score_fn, int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
-    const int64_t* __restrict__ fixed, void* __restrict__ probs, uint8_t* __restrict__ rmap,
-    int64_t* __restrict__ top_idx) {
+    int lane, int64_t t, const float (&lg)[EPL], const KT (&kl)[EPL], const bool (&valid)[EPL],
+    int ldt, int E, int K, int score_fn, int pre_softmax, const float* __restrict__ bias, int G,
+    int GK, float scaling, const int64_t* __restrict__ fixed, void* __restrict__ probs,
+    uint8_t* __restrict__ rmap, int64_t* __restrict__ top_idx) {
   const float NEG = -INFINITY;
-  float sc[EPL], sel[EPL];
+  const KT KNEG = -INFINITY;
+  float sc[EPL];
+  KT sel[EPL];
 
   // Scores.
   if (score_fn == TT_SCORE_SOFTMAX) {
@@ -108,12 +127,13 @@ __device__ __forceinline__ void route_row(
 #pragma unroll
     for (int i = 0; i < EPL; ++i) sc[i] = valid[i] ? sqrtf(softplus_f(lg[i])) : 0.f;
   }
+  const bool raw = score_fn == TT_SCORE_SOFTMAX && !pre_softmax;  // keys: the logits
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane * EPL + i;
     float v = sc[i];
-    if (bias != nullptr && valid[i] && (score_fn != TT_SCORE_SOFTMAX || pre_softmax)) v = v + bias[e];
-    sel[i] = valid[i] ? v : NEG;
+    if (bias != nullptr && valid[i] && !raw) v = v + bias[e];  // fp32 sum
+    sel[i] = valid[i] ? (raw ? kl[i] : (KT)v) : KNEG;
   }
 
   bool taken[EPL];
@@ -123,8 +143,8 @@ __device__ __forceinline__ void route_row(
     taken[i] = false;
     slot[i] = 0;
   }
-  Cand mine;  // lane j < K holds the j-th selected expert
-  mine.sel = NEG;
+  Cand<KT> mine;  // lane j < K holds the j-th selected expert
+  mine.sel = KNEG;
   mine.idx = 0;
   mine.sc = 0.f;
   mine.lg = 0.f;
@@ -170,10 +190,10 @@ __device__ __forceinline__ void route_row(
       bool used[EPL];
 #pragma unroll
       for (int i = 0; i < EPL; ++i) used[i] = false;
-      float gscore = 0.f;
+      KT gscore = 0;
       for (int r = 0; r < m; ++r) {
-        Cand c;
-        c.sel = NEG;
+        Cand<KT> c;
+        c.sel = KNEG;
         c.idx = 0x7fffffff;
         c.sc = 0.f;
         c.lg = 0.f;
@@ -192,10 +212,10 @@ __device__ __forceinline__ void route_row(
       const int group = (lane * EPL) / gs;
       const bool lane_live = lane * EPL < E;
       bool keep = false;
-      float gkey = lane_live ? gscore : NEG;
+      KT gkey = lane_live ? gscore : KNEG;
       for (int r = 0; r < GK; ++r) {
-        Cand c;
-        c.sel = keep ? NEG : gkey;
+        Cand<KT> c;
+        c.sel = keep ? KNEG : gkey;
         c.idx = lane_live ? group : 0x7fffffff;
         c.sc = 0.f;
         c.lg = 0.f;
@@ -204,17 +224,18 @@ __device__ __forceinline__ void route_row(
       }
 #pragma unroll
       for (int i = 0; i < EPL; ++i)
-        if (!keep) sel[i] = NEG;
+        if (!keep) sel[i] = KNEG;
     }
     // k rounds of a wave arg-max. Each lane keeps its head: its best
     // remaining expert (largest key, lowest id on equal keys). A round takes
     // the wave maximum of the heads, the lowest lane holding it (ballot) and
     // that lane's head — larger key first, lower expert id on equal keys, as
     // a comparison of (key, id) pairs would. Only the winning lane advances.
-    float hv = NEG, hsc = 0.f, hlg = 0.f;
+    KT hv = KNEG;
+    float hsc = 0.f, hlg = 0.f;
     int hi = -1;
     auto head = [&]() {
-      hv = NEG;
+      hv = KNEG;
       hi = -1;
 #pragma unroll
       for (int i = 0; i < EPL; ++i)
@@ -233,7 +254,7 @@ __device__ __forceinline__ void route_row(
     };
     head();
     for (int j = 0; j < K; ++j) {
-      const float m = wave_max_uniform(hi >= 0 ? hv : NEG);
+      const KT m = wave_max_uniform(hi >= 0 ? hv : KNEG);
       const uint64_t owners = __ballot(hi >= 0 && hv == m);
       // K <= E valid experts, so some lane still has a head (owners is empty
       // only for NaN keys: lane 0 then reports its head, or -1).
@@ -288,7 +309,7 @@ __device__ __forceinline__ void route_row(
   }
 }
 
-template <int EPL>
+template <int EPL, typename KT>
 __global__ __launch_bounds__(256) void router_fwd_kernel(
     const void* __restrict__ logits, int ldt, int64_t T, int E, int K, int score_fn,
     int pre_softmax, const float* __restrict__ bias, int G, int GK, float scaling,
@@ -298,15 +319,22 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   const int64_t t = (int64_t)blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
   if (t >= T) return;  // whole wave; no block-level synchronisation below
   float lg[EPL];
+  KT kl[EPL];
   bool valid[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane * EPL + i;
     valid[i] = e < E;
-    lg[i] = valid[i] ? load_as_f32(logits, ldt, t * E + e) : -INFINITY;
+    if constexpr (std::is_same<KT, double>::value) {
+      kl[i] = valid[i] ? static_cast<const double*>(logits)[t * E + e] : -INFINITY;
+      lg[i] = (float)kl[i];
+    } else {
+      lg[i] = valid[i] ? load_as_f32(logits, ldt, t * E + e) : -INFINITY;
+      kl[i] = lg[i];
+    }
   }
-  route_row<EPL>(lane, t, lg, valid, ldt, E, K, score_fn, pre_softmax, bias, G, GK, scaling,
-                 fixed, probs, rmap, top_idx);
+  route_row<EPL, KT>(lane, t, lg, kl, valid, ldt, E, K, score_fn, pre_softmax, bias, G, GK,
+                     scaling, fixed, probs, rmap, top_idx);
 }
 
 template <int EPL>
@@ -436,11 +464,12 @@ int loss_blocks(int64_t T) {
 // log-sum-exp of a token's logits as PyTorch forms it: fp32 logits
 // max + log(sum exp(x - max)); bf16 / f16 logits run every step in that
 // dtype (max, x - max, exp, sum, log, + max each rounded), which is what
-// torch.logsumexp does for them. se is the fp32 sum of exp(x - mx).
+// torch.logsumexp does for them. se is the fp32 sum of exp(x - mx). fp64
+// logits take the fp32 form (the z-loss to fp32 precision, not fp64).
 template <int EPL>
 __device__ __forceinline__ float lse_like_torch(const float (&lg)[EPL], const bool (&valid)[EPL],
                                                 float mx, float se, int ldt) {
-  if (ldt == TT_F32) return mx + logf(se);
+  if (ldt == TT_F32 || ldt == TT_F64) return mx + logf(se);
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i)
@@ -647,7 +676,7 @@ __global__ __launch_bounds__(256) void router_loss_bwd_kernel(
       se += ex[i];
     }
     se = wave_sum(se);
-    const bool low = ldt != TT_F32;
+    const bool low = ldt != TT_F32 && ldt != TT_F64;
     float zt[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) zt[i] = 0.f;
@@ -935,8 +964,12 @@ template <int EPL>
 void launch_router_fwd(dim3 g, hipStream_t s, const void* logits, int ldt, int64_t T, int E, int K,
                        int sf, int pre, const float* bias, int G, int GK, float scale,
                        const int64_t* fixed, void* probs, uint8_t* rmap, int64_t* top) {
-  hipLaunchKernelGGL(router_fwd_kernel<EPL>, g, dim3(256), 0, s, logits, ldt, T, E, K, sf, pre,
-                     bias, G, GK, scale, fixed, probs, rmap, top);
+  if (ldt == TT_F64)
+    hipLaunchKernelGGL((router_fwd_kernel<EPL, double>), g, dim3(256), 0, s, logits, ldt, T, E, K,
+                       sf, pre, bias, G, GK, scale, fixed, probs, rmap, top);
+  else
+    hipLaunchKernelGGL((router_fwd_kernel<EPL, float>), g, dim3(256), 0, s, logits, ldt, T, E, K,
+                       sf, pre, bias, G, GK, scale, fixed, probs, rmap, top);
 }
 
 template <int EPL>
@@ -1144,7 +1177,7 @@ __global__ __launch_bounds__(1024) void router_gate_fwd_kernel(
       valid[i] = e < E;
       lg[i] = valid[i] ? L[row * S::LS + e] : -INFINITY;
     }
-    route_row<EPL>(lane, t0 + row, lg, valid, ldt, E, K, score_fn, pre_softmax, bias, G, GK,
+    route_row<EPL>(lane, t0 + row, lg, lg, valid, ldt, E, K, score_fn, pre_softmax, bias, G, GK,
                    scaling, fixed, probs, rmap, top_idx);
   }
 }
@@ -1209,6 +1242,8 @@ int epl_for(int E) {
 }
 
 bool float_dtype(int d) { return d == TT_F32 || d == TT_BF16 || d == TT_F16; }
+// Logits dtypes of the top-k router and its losses (fp64: moe_router_dtype "fp64").
+bool logits_dtype_ok(int d) { return float_dtype(d) || d == TT_F64; }
 
 }  // namespace
 
@@ -1218,7 +1253,7 @@ extern "C" int tt_router_topk_fwd(const void* logits, int logits_dtype, int64_t 
                                   int32_t num_groups, int32_t group_topk, float scaling_factor,
                                   const int64_t* fixed_indices, void* probs,
                                   uint8_t* routing_map, int64_t* top_indices, void* stream) {
-  TT_REQUIRE(float_dtype(logits_dtype), "router: unsupported logits dtype %d", logits_dtype);
+  TT_REQUIRE(logits_dtype_ok(logits_dtype), "router: unsupported logits dtype %d", logits_dtype);
   TT_REQUIRE(num_tokens >= 0, "router: negative token count");
   TT_REQUIRE(num_experts >= 1 && num_experts <= 1024, "router: num_experts must be in [1, 1024]");
   TT_REQUIRE(topk >= 1 && topk <= 64 && topk <= num_experts, "router: topk must be in [1, min(64, E)]");
@@ -1260,7 +1295,7 @@ extern "C" int tt_router_topk_bwd(const void* logits, int logits_dtype, int64_t 
                                   int32_t pre_softmax, float scaling_factor,
                                   const int64_t* top_indices, const void* grad_probs,
                                   void* grad_logits, void* stream) {
-  TT_REQUIRE(float_dtype(logits_dtype), "router_bwd: unsupported logits dtype %d", logits_dtype);
+  TT_REQUIRE(logits_dtype_ok(logits_dtype), "router_bwd: unsupported logits dtype %d", logits_dtype);
   TT_REQUIRE(num_experts >= 1 && num_experts <= 1024, "router_bwd: num_experts must be in [1, 1024]");
   TT_REQUIRE(topk >= 1 && topk <= 64 && topk <= num_experts, "router_bwd: bad topk");
   TT_REQUIRE(score_function >= 0 && score_function <= 2, "router_bwd: bad score function");
@@ -1383,7 +1418,8 @@ extern "C" int tt_router_loss_fwd(const void* logits, int logits_dtype, int64_t 
                                   const uint8_t* padding_mask, float* prob_sum,
                                   int64_t* tokens_per_expert, float* z_sum, void* workspace,
                                   size_t workspace_bytes, void* stream) {
-  TT_REQUIRE(float_dtype(logits_dtype), "router_loss: unsupported logits dtype %d", logits_dtype);
+  TT_REQUIRE(logits_dtype_ok(logits_dtype), "router_loss: unsupported logits dtype %d",
+             logits_dtype);
   TT_REQUIRE(num_tokens >= 0, "router_loss: negative token count");
   TT_REQUIRE(num_experts >= 1 && num_experts <= 1024,
              "router_loss: num_experts must be in [1, 1024]");
@@ -1428,7 +1464,7 @@ extern "C" int tt_router_loss_bwd(const void* logits, int logits_dtype, int64_t 
                                   int32_t num_experts, int32_t score_function,
                                   const uint8_t* padding_mask, const float* grad_prob_sum,
                                   const float* grad_z_sum, void* grad_logits, void* stream) {
-  TT_REQUIRE(float_dtype(logits_dtype), "router_loss_bwd: unsupported logits dtype %d",
+  TT_REQUIRE(logits_dtype_ok(logits_dtype), "router_loss_bwd: unsupported logits dtype %d",
              logits_dtype);
   TT_REQUIRE(num_tokens >= 0, "router_loss_bwd: negative token count");
   TT_REQUIRE(num_experts >= 1 && num_experts <= 1024,

@@ -164,16 +164,14 @@ class TopKRouter(Router):
         super().__init__(config=config)
         # Limits of the HIP top-k kernels (one wave per token, up to 16 experts
         # per lane, a k-round selection), stated here so that a layer the GPU
-        # cannot route fails when it is built, not on its first call.
+        # cannot route fails when it is built, not on its first call. Router
+        # dtypes fp32, fp64 and the input dtype are all supported.
         if config.num_moe_experts > MAX_EXPERTS:
             raise ValueError(f"TopKRouter: num_moe_experts={config.num_moe_experts} exceeds the "
                              f"{MAX_EXPERTS} experts the router kernels support")
         if config.moe_router_topk > MAX_TOPK:
             raise ValueError(f"TopKRouter: moe_router_topk={config.moe_router_topk} exceeds the "
                              f"{MAX_TOPK} the router kernels support")
-        if config.moe_router_dtype == "fp64":
-            raise ValueError("TopKRouter: moe_router_dtype='fp64' is not supported by the router "
-                             "kernels (fp32 or the input dtype)")
         self.topk = config.moe_router_topk
         self.routing_type = config.moe_router_load_balancing_type
         self.score_function = config.moe_router_score_function
