@@ -273,7 +273,7 @@ int tt_gmm_wgrad(const void* x, const void* dy, int dtype, int64_t m, int64_t k,
  * activations; the result equals tt_gmm_fwd / tt_gmm_dgrad on the gathered
  * rows bit for bit. bf16 / f16, R a multiple of 64 above 64, sources under
  * 2 GiB; other problems return TT_ERR_INVALID. A src_of_row entry outside
- * [0, src_rows) reads a row of zeros (the loads are bounded by the source). */
+ * [0, src_rows) (negative included) reads a row of zeros. */
 int tt_gmm_fwd_gather(const void* x_src, int64_t src_rows, const int32_t* src_of_row,
                       const void* w, int dtype, int64_t m, int64_t k, int64_t n,
                       int32_t num_experts, int32_t trans_b, const int64_t* counts, void* y,
@@ -292,6 +292,15 @@ int tt_gmm_wgrad_gather(const void* x, int64_t x_src_rows, const int32_t* x_src_
                         const void* dy, int64_t dy_src_rows, const int32_t* dy_src_of_row,
                         int dtype, int64_t m, int64_t k, int64_t n, int32_t num_experts,
                         int32_t trans_b, const int64_t* counts, void* dw, void* stream);
+/* Whether a gathering entry point takes a problem (1) or returns
+ * TT_ERR_INVALID for its shape (0), without launching: op 0
+ * tt_gmm_fwd_gather (x_src [src_rows, k]), 1 tt_gmm_dgrad_gather (dy_src
+ * [src_rows, n]), 2 / 3 tt_gmm_wgrad_gather with the rows of x / of dy
+ * gathered. No counterpart in the reference: the layer asks it before taking
+ * the folded-permutation path, so shapes the gathering kernels do not cover
+ * (e.g. more experts than their LDS schedule holds) keep the permutation. */
+int tt_gmm_gather_supported(int32_t op, int dtype, int64_t src_rows, int64_t m, int64_t k,
+                            int64_t n, int32_t num_experts);
 
 /* FP8 e4m3 weights with 128x128 block scales, HF [out, in] orientation:
  * qw [E, N, K] bytes, scale [E, ceil(N/128), ceil(K/128)] (bf16 or f32).

@@ -132,6 +132,59 @@ def test_gathered_wgrad_equals_the_packed_wgrad(dtype, trans_b, which, E, M, T, 
         assert torch.equal(dw_g, dw_p)
 
 
+def test_gathered_rows_out_of_range_read_zeros():
+    """Row-map entries outside [0, src_rows) (-1, src_rows, 2^30) read rows of
+    zeros in every gathering GEMM: the results equal the packed GEMMs with zero
+    rows there (the header's contract), not a wrapped-around source row."""
+    from torchturbo_amd import _lib
+
+    dtype, E, M, T, K, N = torch.bfloat16, 13, 9000, 2000, 512, 768
+    counts = _loads(E, M, seed=77)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    rows = torch.randint(0, T, (M,), generator=g, device=DEV, dtype=torch.int32)
+    bad = torch.randperm(M, generator=g, device=DEV)[:M // 20]
+    rows[bad[0::3]] = -1
+    rows[bad[1::3]] = T
+    rows[bad[2::3]] = 1 << 30
+    inside = (rows >= 0) & (rows < T)
+    eff = torch.where(inside, rows, torch.full_like(rows, T)).long()
+    xs = torch.randn(T, K, generator=g, device=DEV).to(dtype)
+    dys = torch.randn(T, N, generator=g, device=DEV).to(dtype)
+    x_packed = torch.cat([xs, xs.new_zeros(1, K)])[eff]
+    dy_packed = torch.cat([dys, dys.new_zeros(1, N)])[eff]
+    w = (torch.randn(E, K, N, generator=g, device=DEV) * 0.05).to(dtype)
+    cnt = counts.to(DEV)
+    args = (_lib.dtype_code(dtype), M, K, N, E, 0, _lib.ptr(cnt))
+    st = _lib.stream()
+    y_p, y_g = (torch.empty(M, N, dtype=dtype, device=DEV) for _ in range(2))
+    dx_p, dx_g = (torch.empty(M, K, dtype=dtype, device=DEV) for _ in range(2))
+    _lib.call("tt_gmm_fwd", _lib.ptr(x_packed), _lib.ptr(w), *args, _lib.ptr(y_p), st)
+    _lib.call("tt_gmm_dgrad", _lib.ptr(dy_packed), _lib.ptr(w), *args, _lib.ptr(dx_p), st)
+    _lib.call("tt_gmm_fwd_gather", _lib.ptr(xs), T, _lib.ptr(rows), _lib.ptr(w), *args,
+              _lib.ptr(y_g), st)
+    _lib.call("tt_gmm_dgrad_gather", _lib.ptr(dys), T, _lib.ptr(rows), _lib.ptr(w), *args,
+              _lib.ptr(dx_g), st)
+    torch.cuda.synchronize()
+    assert torch.equal(y_g, y_p)
+    assert torch.equal(dx_g, dx_p)
+    assert not y_g[~inside].any()
+    other_dy = torch.randn(M, N, generator=g, device=DEV).to(dtype)
+    other_x = torch.randn(M, K, generator=g, device=DEV).to(dtype)
+    for which in ("x", "dy"):
+        xp, dyp = (x_packed, other_dy) if which == "x" else (other_x, dy_packed)
+        dw_p = torch.empty(E, K, N, dtype=dtype, device=DEV)
+        dw_g = torch.full((E, K, N), float("nan"), dtype=dtype, device=DEV)
+        _lib.call("tt_gmm_wgrad", _lib.ptr(xp), _lib.ptr(dyp), *args, _lib.ptr(dw_p), st)
+        if which == "x":
+            _lib.call("tt_gmm_wgrad_gather", _lib.ptr(xs), T, _lib.ptr(rows), _lib.ptr(other_dy),
+                      0, None, *args, _lib.ptr(dw_g), st)
+        else:
+            _lib.call("tt_gmm_wgrad_gather", _lib.ptr(other_x), 0, None, _lib.ptr(dys), T,
+                      _lib.ptr(rows), *args, _lib.ptr(dw_g), st)
+        torch.cuda.synchronize()
+        assert torch.equal(dw_g, dw_p), which
+
+
 def test_gathered_wgrad_rejects_short_reductions():
     """At most 512 rows per expert on average the persistent weight-gradient kernel
     runs, which has no gathered path: the call fails before any launch."""

@@ -621,11 +621,13 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
     dma4((uint32_t)((t.seg0 + row) * 4), irsrc,
          lds_addr_of((lds_char*)gidx) + (uint32_t)((wv * 2 + (grp & 1)) * 256));
   };
+  const uint32_t gsrc = (uint32_t)gsrc_rows;
   auto offsets = [&](int kk) {  // byte offsets of k-tile kk's chunks from its rows
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int row = kk * DM_BK + 2 * (wv * 8 + q) + (lane >> 5);
-      gof[q] = row < kvalid ? grow_v[q] * ld2 + gcol[q & 1] : DM_OOB;
+      // rows past the expert and entries outside [0, gsrc_rows) read zeros
+      gof[q] = row < kvalid && grow_v[q] < gsrc ? grow_v[q] * ld2 + gcol[q & 1] : DM_OOB;
     }
   };
   auto read_rows = [&](int kk) {  // source rows of k-tile kk's eight chunks
@@ -1219,7 +1221,9 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       const int64_t row = r0 + 8 * q;
       const int64_t at = t.seg0 + row;
       const uint32_t v = (uint32_t)arow[at < M ? at : M - 1];
-      ro[q] = row < t.nrows ? v : GA_NOROW;
+      // An entry outside [0, asrc_rows) (a negative id reads as a large
+      // unsigned value) reads a row of zeros, like a row past the expert.
+      ro[q] = row < t.nrows && v < (uint32_t)asrc_rows ? v : GA_NOROW;
     }
   };
   auto gather_offsets = [&](uint32_t (&ro)[8]) {
@@ -1453,7 +1457,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
         const int64_t row = tc.i0 + 8 * (2 * wave + p) + (lane >> 3);
         const int64_t at = tc.seg0 + row;
         const uint32_t v = (uint32_t)arow[at < M ? at : M - 1];
-        tro[p] = row < tc.nrows ? v * (uint32_t)(lda * 2) : GA_NOROW;
+        tro[p] = row < tc.nrows && v < (uint32_t)asrc_rows ? v * (uint32_t)(lda * 2) : GA_NOROW;
       }
     }
     auto thin_b = [&](int k) {  // weight k-tile k into ring slot k % 3
@@ -2479,6 +2483,39 @@ int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K,
   return launch_mfma_k<MODE, TB, ET, false>(p0, p1, out, M, K, N, E, counts, s, nblk, ti, tj);
 }
 
+// Shape limits of the gathering launches, shared by the launchers and
+// tt_gmm_gather_supported: nullptr when the problem is taken, else what
+// rules it out.
+const char* gather_limit(int MODE, int64_t src_rows, int64_t M, int64_t K, int64_t N, int E) {
+  const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length = source row length
+  const int64_t J = MODE == MODE_FWD ? N : K;  // output width
+  if (!(R > P_BK && R % P_BK == 0))
+    return "the reduction length must be a multiple of 64 above 64";
+  if (p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI > 160 * 1024)
+    return "too many experts for the LDS tile schedule";
+  if (!(src_rows >= 1 && (src_rows * R + 4 * P_BK) * 2 < (int64_t)GA_NOROW))
+    return "the source must hold at least one row and less than 2 GiB";
+  if (!((M + DM_BM) * J * 2 < (int64_t)DM_OOB && K * N * 2 < (int64_t)DM_OOB &&
+        (R + 2 * P_BK) * J * 2 < (int64_t)DM_OOB))
+    return "operands of 4 GiB or more are not supported";
+  return nullptr;
+}
+// GX: 1 when the rows of x are gathered, 2 for the rows of dy.
+const char* wgrad_gather_limit(int GX, int64_t src_rows, int64_t M, int64_t K, int64_t N, int E) {
+  if (!(M > (int64_t)E * P_WGRAD_ROWS))
+    return "weight gradients with gathered rows need more than 512 rows per expert on average";
+  if (schedule_bytes(E) + (size_t)DM_ST * DM_STAGE + 1024 > 160 * 1024)
+    return "too many experts for the LDS tile schedule";
+  const int64_t ld = K > N ? K : N;
+  if (!((M + DM_BM) * ld * 2 < (int64_t)DM_OOB && K * N * 2 < (int64_t)DM_OOB &&
+        M * 4 < (int64_t)DM_OOB))
+    return "operands of 4 GiB or more are not supported";
+  const int64_t gld = GX == 1 ? K : N;
+  if (!(src_rows >= 1 && (src_rows + 1) * gld * 2 < (int64_t)DM_OOB))
+    return "the source must hold at least one row and less than 4 GiB";
+  return nullptr;
+}
+
 // fwd / dgrad with gathered A rows (persistent kernel only): A row r is row
 // arow[r] of src ([src_rows, R], R the reduction length).
 template <int MODE, bool TB, int ET>
@@ -2488,19 +2525,9 @@ int launch_gather(const void* src, int64_t src_rows, const int32_t* arow, const 
   const int64_t nblk = grid_blocks(MODE, TB, M, K, N, E, DM_BM, DM_BN, ti, tj);
   if (nblk == 0) return TT_OK;
   TT_REQUIRE(nblk < 0x7fffffff, "gmm: grid too large");
-  const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length = source row length
-  const int64_t J = MODE == MODE_FWD ? N : K;  // output width
-  TT_REQUIRE(R > P_BK && R % P_BK == 0,
-             "gmm gather: the reduction length must be a multiple of %d above %d (got %lld)",
-             P_BK, P_BK, (long long)R);
-  TT_REQUIRE(p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI <= 160 * 1024,
-             "gmm gather: too many experts for the LDS tile schedule");
-  TT_REQUIRE(src_rows >= 1 && (src_rows * R + 4 * P_BK) * 2 < (int64_t)GA_NOROW,
-             "gmm gather: the source must hold at least one row and less than 2 GiB");
-  TT_REQUIRE((M + DM_BM) * J * 2 < (int64_t)DM_OOB && K * N * 2 < (int64_t)DM_OOB &&
-                 (R + 2 * P_BK) * J * 2 < (int64_t)DM_OOB,
-             "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
-             (long long)M, (long long)K, (long long)N);
+  const char* why = gather_limit(MODE, src_rows, M, K, N, E);
+  TT_REQUIRE(why == nullptr, "gmm gather: %s (M=%lld K=%lld N=%lld E=%d, %lld source rows)", why,
+             (long long)M, (long long)K, (long long)N, E, (long long)src_rows);
   return launch_p64_k<MODE, TB, ET, false, true>(src, w, out, M, K, N, E, counts, s, nblk, ti, tj,
                                                  arow, src_rows);
 }
@@ -2516,20 +2543,9 @@ int launch_wgrad_gather(const void* x, const void* dy, int64_t src_rows, const i
   const int64_t nblk = grid_blocks(MODE_WGRAD, TB, M, K, N, E, DM_BM, DM_BN, ti, tj);
   if (nblk == 0) return TT_OK;
   TT_REQUIRE(nblk < 0x7fffffff, "gmm: grid too large");
-  TT_REQUIRE(M > (int64_t)E * P_WGRAD_ROWS,
-             "gmm gather: weight gradients with gathered rows need more than %lld rows per "
-             "expert on average (M=%lld, E=%d)",
-             (long long)P_WGRAD_ROWS, (long long)M, E);
-  TT_REQUIRE(schedule_bytes(E) + (size_t)DM_ST * DM_STAGE + 1024 <= 160 * 1024,
-             "gmm: too many experts for the LDS tile schedule");
-  const int64_t ld = K > N ? K : N;
-  const int64_t gld = GX == 1 ? K : N;
-  TT_REQUIRE((M + DM_BM) * ld * 2 < (int64_t)DM_OOB && K * N * 2 < (int64_t)DM_OOB &&
-                 M * 4 < (int64_t)DM_OOB,
-             "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
-             (long long)M, (long long)K, (long long)N);
-  TT_REQUIRE(src_rows >= 1 && (src_rows + 1) * gld * 2 < (int64_t)DM_OOB,
-             "gmm gather: the source must hold at least one row and less than 4 GiB");
+  const char* why = wgrad_gather_limit(GX, src_rows, M, K, N, E);
+  TT_REQUIRE(why == nullptr, "gmm gather: %s (M=%lld K=%lld N=%lld E=%d, %lld source rows)", why,
+             (long long)M, (long long)K, (long long)N, E, (long long)src_rows);
   return launch_mfma_k<MODE_WGRAD, TB, ET, false, GX>(x, dy, dw, M, K, N, E, counts, s, nblk, ti,
                                                       tj, grow, src_rows);
 }
@@ -2756,6 +2772,20 @@ extern "C" int tt_gmm_fp8_dgrad(const void* dy, const uint8_t* qw, const void* s
   if (rc != TT_OK) return rc;
   return launch_fp8<MODE_DGRAD>(dy, qw, scale, scale_dtype, dx, m, k, n, num_experts, counts,
                                S(stream));
+}
+
+extern "C" int tt_gmm_gather_supported(int32_t op, int dtype, int64_t src_rows, int64_t m,
+                                       int64_t k, int64_t n, int32_t num_experts) {
+  if ((dtype != TT_BF16 && dtype != TT_F16) || m < 0 || k <= 0 || n <= 0 || k % 8 || n % 8 ||
+      num_experts < 1 || num_experts > 4096)
+    return 0;
+  switch (op) {
+    case 0: return gather_limit(MODE_FWD, src_rows, m, k, n, num_experts) == nullptr;
+    case 1: return gather_limit(MODE_DGRAD, src_rows, m, k, n, num_experts) == nullptr;
+    case 2: return wgrad_gather_limit(1, src_rows, m, k, n, num_experts) == nullptr;
+    case 3: return wgrad_gather_limit(2, src_rows, m, k, n, num_experts) == nullptr;
+    default: return 0;
+  }
 }
 
 extern "C" int tt_gmm_fwd_gather(const void* x_src, int64_t src_rows, const int32_t* src_of_row,

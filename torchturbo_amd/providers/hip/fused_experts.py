@@ -181,12 +181,24 @@ def eligible(tokens: torch.Tensor, w1: torch.Tensor, topk: int, num_experts: int
 
 def shapes_pay(tokens: int, hidden: int, fc1_width: int, topk: int, num_experts: int,
                dtype: torch.dtype) -> bool:
-    """The shape part of ``eligible``: 16-bit activations, a hidden size the
-    gathering fwd / dgrad kernel covers (a multiple of 64 above 64), more than
-    512 routed rows per expert on average (the gathering weight-gradient
-    kernel) and fc1 at most twice as wide as the hidden size."""
-    return (dtype in (torch.bfloat16, torch.float16) and hidden > 64 and hidden % 64 == 0
-            and tokens * topk > 512 * num_experts and fc1_width <= 2 * hidden)
+    """The shape part of ``eligible``: fc1 at most twice as wide as the hidden
+    size (where gathering pays), and every gathering GEMM of the layer takes
+    the shapes, as the library reports without launching
+    (``tt_gmm_gather_supported``): fc1 forward with gathered token rows
+    ([T, H] source, reduction H), fc1's weight gradient with gathered x rows,
+    fc2's data gradient with gathered output-gradient rows (reduction H) and
+    fc2's weight gradient with gathered output-gradient rows (more than 512
+    routed rows per expert on average, 16-bit, reductions a multiple of 64
+    above 64, the experts' schedule in LDS)."""
+    if dtype not in (torch.bfloat16, torch.float16) or fc1_width > 2 * hidden:
+        return False
+    lib = L.load()
+    code = L.dtype_code(dtype)
+    m = tokens * topk
+    ffn = fc1_width // 2
+    return all(lib.tt_gmm_gather_supported(op, code, tokens, m, k, n, num_experts) == 1
+               for op, k, n in ((0, hidden, fc1_width), (2, hidden, fc1_width),
+                                (1, ffn, hidden), (3, ffn, hidden)))
 
 
 def grouped_mlp_tokens(experts, tokens, probs, routing_map, expert_indices):
