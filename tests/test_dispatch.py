@@ -192,3 +192,21 @@ def test_hip_providers_registered_for_cuda_only():
     assert all(s.devices == (TurboDevice.CUDA,) and s.kind == OpImplKind.CUSTOM
                and s.priority > 100 for s in hip)
 
+
+
+def test_one_impl_name_defined_by_two_classes_is_an_error():
+    """Two provider classes carrying the same impl_name (ops/dispatcher.py:77-97):
+    building a dispatcher over both modules raises ValueError naming both."""
+    reg = OpRegistry()
+    make_provider_module("fake_dup_a", reg, [("dup_impl", "opd", OpImplKind.NATIVE, 0, (), True, 1)])
+    make_provider_module("fake_dup_b", reg, [("dup_impl", "opd", OpImplKind.NATIVE, 0, (), True, 2)])
+    add_provider_package("fake_dup_a")
+    add_provider_package("fake_dup_b")
+    try:
+        with pytest.raises(ValueError, match="defined by both fake_dup_a.dup_impl and fake_dup_b.dup_impl"):
+            OpDispatcher(device_runtime=CpuRuntime(), registry=reg)
+    finally:
+        remove_provider_package("fake_dup_a")
+        remove_provider_package("fake_dup_b")
+        sys.modules.pop("fake_dup_a", None)
+        sys.modules.pop("fake_dup_b", None)

@@ -2,13 +2,14 @@
 
 Selection semantics follow ``src/torchturbo/ops/dispatcher.py:108-293``:
 
-* ``_configure`` resolves every registered op for the runtime's device and
+* construction resolves every registered op for the runtime's device and
   records (does not raise on) unresolved ones; an invalid config override
   raises ``RuntimeError`` at construction;
 * an explicit ``impl=`` or an override never falls back (``148-160``);
 * ``native`` / ``custom`` policies filter by kind and never cross over;
   ``auto`` walks the ranked candidates past unavailable ones (``162-186``);
-* the first available candidate per (op, device, impl) is cached.
+* the first available candidate per (op, explicit impl) is remembered (a
+  dispatcher serves one device).
 
 Facades (``moe_permutation`` ``530-590``, ``moe_unpermutation`` ``592-637``,
 ``moe_sort_chunks`` ``639-660``, ``grouped_matmul`` ``311-327``,
@@ -22,13 +23,11 @@ from __future__ import annotations
 import importlib
 import logging
 from collections.abc import Mapping
-from dataclasses import dataclass
-from types import ModuleType
 from typing import Any
 
 import torch
 
-from ..runtime import DeviceRuntime, TurboDevice
+from ..runtime import DeviceRuntime
 from .base import OpImpl, OpImplKind, OpPolicy, OpSpec
 from .moe import MoEPermutation, get_expert_indices
 from .providers import iter_provider_modules
@@ -37,11 +36,29 @@ from .registry import OpRegistry
 logger = logging.getLogger("torchturbo_amd")
 
 
-@dataclass(frozen=True)
-class _Candidate:
-    impl: OpImpl
-    spec: OpSpec
-    fallback: bool
+def _impl_classes_of(module_names) -> dict[str, type[OpImpl]]:
+    """impl_name -> ``OpImpl`` subclass, over the classes that the given
+    provider modules define themselves (not import) and that carry an
+    ``OpSpec``. One impl_name bound to two different classes is an error."""
+    found: dict[str, list[type[OpImpl]]] = {}
+    for module_name in module_names:
+        module = importlib.import_module(module_name)
+        for obj in vars(module).values():
+            if (isinstance(obj, type) and obj is not OpImpl and issubclass(obj, OpImpl)
+                    and obj.__module__ == module.__name__
+                    and getattr(obj, "__op_spec__", None) is not None):
+                bucket = found.setdefault(obj.__op_spec__.impl_name, [])
+                if obj not in bucket:
+                    bucket.append(obj)
+    for impl_name, bucket in found.items():
+        if len(bucket) > 1:
+            first, second = bucket[0], bucket[1]
+            raise ValueError(
+                f"Op implementation {impl_name!r} is defined by both "
+                f"{first.__module__}.{first.__qualname__} and "
+                f"{second.__module__}.{second.__qualname__}."
+            )
+    return {impl_name: bucket[0] for impl_name, bucket in found.items()}
 
 
 class OpDispatcher:
@@ -62,11 +79,14 @@ class OpDispatcher:
         if any(not isinstance(k, str) or not isinstance(v, str)
                for k, v in self._overrides.items()):
             raise TypeError("overrides must map op names to implementation names.")
-        self._impls: dict[str, OpImpl] = {}
-        self._impl_classes: dict[str, type[OpImpl]] = {}
-        self._cache: dict[tuple[str, str, str | None], _Candidate] = {}
+        self._device = device_runtime.turbo_device
+        self._impl_classes = _impl_classes_of(iter_provider_modules(self._device))
+        self._instances: dict[str, OpImpl] = {}
+        # (op, explicit impl or None) -> (chosen spec, whether ranked candidates
+        # before it were unavailable)
+        self._chosen: dict[tuple[str, str | None], tuple[OpSpec, bool]] = {}
         self._unresolved_ops: dict[str, str] = {}
-        self._configure()
+        self._resolve_all()
 
     @property
     def device_runtime(self) -> DeviceRuntime:
@@ -84,128 +104,103 @@ class OpDispatcher:
     def unresolved_ops(self) -> dict[str, str]:
         return dict(self._unresolved_ops)
 
-    # -- provider indexing -------------------------------------------------
-    @staticmethod
-    def _index_provider_module(module: ModuleType, classes: dict[str, type[OpImpl]]) -> None:
-        for value in module.__dict__.values():
-            if not isinstance(value, type) or value.__module__ != module.__name__:
-                continue
-            if not issubclass(value, OpImpl) or value is OpImpl:
-                continue
+    # -- resolution --------------------------------------------------------
+    def _resolve_all(self) -> None:
+        """Resolve every op the device has providers for. Overrides are checked
+        first and a bad one raises; an op with no usable implementation is only
+        recorded (it raises when called)."""
+        here = self.registry.list(lambda s: not s.devices or self._device in s.devices)
+        provided = {s.op_name for s in here if s.impl_name in self._impl_classes}
+        for op_name, impl_name in sorted(self._overrides.items()):
             try:
-                spec = value.op_spec()
-            except RuntimeError:
-                continue
-            existing = classes.get(spec.impl_name)
-            if existing is not None and existing is not value:
-                raise ValueError(
-                    f"Op implementation {spec.impl_name!r} is defined by both "
-                    f"{existing.__module__}.{existing.__qualname__} and "
-                    f"{value.__module__}.{value.__qualname__}."
-                )
-            classes[spec.impl_name] = value
-
-    def _configure(self) -> None:
-        device = self._device_runtime.turbo_device
-        classes: dict[str, type[OpImpl]] = {}
-        for name in iter_provider_modules(device):
-            self._index_provider_module(importlib.import_module(name), classes)
-        self._impl_classes = classes
-        specs = self.registry.list(lambda s: not s.devices or device in s.devices)
-        op_names = {s.op_name for s in specs if s.impl_name in classes}
-        op_names.update(self._overrides)
-        for op_name in sorted(op_names):
-            override = self._overrides.get(op_name)
-            try:
-                self._candidate_impl(op_name, device, impl=override)
+                self._resolve(op_name, impl_name)
             except RuntimeError as exc:
-                if override is not None:
-                    raise RuntimeError(
-                        f"Invalid override for op {op_name!r}: {override!r}. {exc}"
-                    ) from exc
+                raise RuntimeError(
+                    f"Invalid override for op {op_name!r}: {impl_name!r}. {exc}"
+                ) from exc
+        for op_name in sorted(provided - set(self._overrides)):
+            try:
+                self._resolve(op_name, None)
+            except RuntimeError as exc:
                 self._unresolved_ops[op_name] = str(exc)
 
-    # -- selection ---------------------------------------------------------
-    def _candidate_impl(self, op_name: str, device: TurboDevice, impl: str | None = None) -> OpImpl:
-        key = (op_name, device.value, impl)
-        cached = self._cache.get(key)
-        if cached is not None:
-            return cached.impl
-        if impl is not None:
-            spec = self.registry.get_by_impl_name(impl)
-            if spec.op_name != op_name:
-                raise RuntimeError(
-                    f"Implementation {impl!r} is registered for op {spec.op_name!r}, "
-                    f"not {op_name!r}."
-                )
-            if spec.devices and device not in spec.devices:
-                raise RuntimeError(
-                    f"Implementation {impl!r} for op {op_name!r} does not support "
-                    f"device={device.value}."
-                )
-            specs = [spec]
-        else:
-            policy = self._default_policy
+    def _policy_admits(self, spec: OpSpec) -> bool:
+        if self._default_policy == OpPolicy.NATIVE:
+            return spec.kind == OpImplKind.NATIVE
+        if self._default_policy == OpPolicy.CUSTOM:
+            return spec.kind == OpImplKind.CUSTOM
+        return True
 
-            def matches(spec: OpSpec) -> bool:
-                if spec.op_name != op_name or spec.impl_name not in self._impl_classes:
-                    return False
-                if spec.devices and device not in spec.devices:
-                    return False
-                if policy == OpPolicy.NATIVE:
-                    return spec.kind == OpImplKind.NATIVE
-                if policy == OpPolicy.CUSTOM:
-                    return spec.kind == OpImplKind.CUSTOM
-                return True
+    def _ranked(self, op_name: str, impl: str | None) -> list[OpSpec]:
+        """The specs to try for ``op_name``: the named one only (no fallback), or
+        the policy's candidates for this device, best first."""
+        device = self._device
+        if impl is None:
+            return self.registry.list(
+                lambda s: (s.op_name == op_name and s.impl_name in self._impl_classes
+                           and (not s.devices or device in s.devices)
+                           and self._policy_admits(s)))
+        spec = self.registry.get_by_impl_name(impl)
+        if spec.op_name != op_name:
+            raise RuntimeError(
+                f"Implementation {impl!r} is registered for op {spec.op_name!r}, not {op_name!r}."
+            )
+        if spec.devices and device not in spec.devices:
+            raise RuntimeError(
+                f"Implementation {impl!r} for op {op_name!r} does not support "
+                f"device={device.value}."
+            )
+        return [spec]
 
-            specs = self.registry.list(matches)
-
-        unavailable: list[str] = []
-        for spec in specs:
-            impl_obj = self._load_impl(spec)
-            if not impl_obj.available():
-                unavailable.append(spec.impl_name)
-                continue
-            self._cache[key] = _Candidate(impl_obj, spec, bool(unavailable))
-            return impl_obj
-        detail = f" (unavailable={unavailable})" if unavailable else ""
-        selected = f"policy={self._default_policy.value}" if impl is None else f"impl={impl}"
-        raise RuntimeError(
-            f"No implementation for op={op_name!r}, device={device.value}, {selected}{detail}."
-        )
-
-    def _load_impl(self, spec: OpSpec) -> OpImpl:
-        impl = self._impls.get(spec.impl_name)
-        if impl is not None:
-            return impl
+    def _instance(self, spec: OpSpec) -> OpImpl:
+        try:
+            return self._instances[spec.impl_name]
+        except KeyError:
+            pass
         cls = self._impl_classes.get(spec.impl_name)
         if cls is None:
             raise RuntimeError(f"No OpImpl class registered for impl_name {spec.impl_name!r}.")
-        impl = cls()
-        self._impls[spec.impl_name] = impl
-        return impl
+        return self._instances.setdefault(spec.impl_name, cls())
+
+    def _resolve(self, op_name: str, impl: str | None) -> OpImpl:
+        """The implementation ``op_name`` runs (first available candidate,
+        remembered per (op, explicit impl))."""
+        hit = self._chosen.get((op_name, impl))
+        if hit is not None:
+            return self._instances[hit[0].impl_name]
+        skipped = []
+        for spec in self._ranked(op_name, impl):
+            obj = self._instance(spec)
+            if obj.available():
+                self._chosen[(op_name, impl)] = (spec, bool(skipped))
+                return obj
+            skipped.append(spec.impl_name)
+        how = f"policy={self._default_policy.value}" if impl is None else f"impl={impl}"
+        why = f" (unavailable={skipped})" if skipped else ""
+        raise RuntimeError(
+            f"No implementation for op={op_name!r}, device={self._device.value}, {how}{why}."
+        )
 
     def selected_impl_name(self, op_name: str) -> str:
         """Name of the implementation the dispatcher would run for ``op_name``."""
-        device = self._device_runtime.turbo_device
         override = self._overrides.get(op_name)
-        self._candidate_impl(op_name, device, impl=override)
-        return self._cache[(op_name, device.value, override)].spec.impl_name
+        self._resolve(op_name, override)
+        return self._chosen[(op_name, override)][0].impl_name
 
     def log_ops_selection(self) -> str:
         """Log (and return) the op → implementation table (``dispatcher.py:213-277``)."""
         rows = []
-        chosen = {op: c for (op, _, impl), c in self._cache.items()
+        chosen = {op: hit for (op, impl), hit in self._chosen.items()
                   if impl == self._overrides.get(op)}
         for op_name in sorted(set(chosen) | set(self._unresolved_ops)):
-            cand = chosen.get(op_name)
-            if cand is None:
+            hit = chosen.get(op_name)
+            if hit is None:
                 rows.append((op_name, "-", "-", "-", "unavailable"))
                 continue
+            spec, fell_back = hit
             status = ("overridden" if op_name in self._overrides
-                      else "fallback" if cand.fallback else "selected")
-            rows.append((op_name, cand.spec.impl_name, cand.spec.kind.value,
-                         str(cand.spec.priority), status))
+                      else "fallback" if fell_back else "selected")
+            rows.append((op_name, spec.impl_name, spec.kind.value, str(spec.priority), status))
         if not rows:
             rows.append(("<no registered ops>", "-", "-", "-", "-"))
         headers = ("Op", "Implementation", "Kind", "Priority", "Status")
@@ -222,9 +217,8 @@ class OpDispatcher:
         return text
 
     def _dispatch(self, op_name: str, *args: Any, impl: str | None = None, **kwargs: Any):
-        device = self._device_runtime.turbo_device
         selected = impl if impl is not None else self._overrides.get(op_name)
-        return self._candidate_impl(op_name, device, impl=selected)(*args, **kwargs)
+        return self._resolve(op_name, selected)(*args, **kwargs)
 
     # -- MoE facades -------------------------------------------------------
     def grouped_matmul(self, x, weight, group_list, *, trans_b: bool = False,
