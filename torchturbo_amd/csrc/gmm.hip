@@ -626,16 +626,21 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int row = kk * DM_BK + 2 * (wv * 8 + q) + (lane >> 5);
-      // rows past the expert and entries outside [0, gsrc_rows) read zeros
-      gof[q] = row < kvalid && grow_v[q] < gsrc ? grow_v[q] * ld2 + gcol[q & 1] : DM_OOB;
+      gof[q] = row < kvalid ? grow_v[q] * ld2 + gcol[q & 1] : DM_OOB;
     }
   };
   auto read_rows = [&](int kk) {  // source rows of k-tile kk's eight chunks
     lds_char* const ring = (lds_char*)gidx + (wv * 2 + ((kk >> 2) & 1)) * 256;
     const uint32_t at = (uint32_t)(((kk & 3) * 16 + (lane >> 5) * 8) * 4);
     const uint4 i0 = read_k(ring, at), i1 = read_k(ring, at + 16);
-    grow_v[0] = i0.x; grow_v[1] = i0.y; grow_v[2] = i0.z; grow_v[3] = i0.w;
-    grow_v[4] = i1.x; grow_v[5] = i1.y; grow_v[6] = i1.z; grow_v[7] = i1.w;
+    // An entry outside [0, gsrc_rows) (a negative one reads as a large
+    // unsigned value) becomes gsrc_rows: its offset lies past the source's
+    // resource, so it reads a row of zeros (the launch bounds
+    // (gsrc_rows + 1) * ld * 2 below 4 GiB, so the offset does not wrap).
+    grow_v[0] = min(i0.x, gsrc); grow_v[1] = min(i0.y, gsrc);
+    grow_v[2] = min(i0.z, gsrc); grow_v[3] = min(i0.w, gsrc);
+    grow_v[4] = min(i1.x, gsrc); grow_v[5] = min(i1.y, gsrc);
+    grow_v[6] = min(i1.z, gsrc); grow_v[7] = min(i1.w, gsrc);
   };
 
   // Chunk q of k-tile kt into stage `stg`.
