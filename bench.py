@@ -39,6 +39,7 @@ HBM_PEAK_GBS = 8000.0
 GEMM_ENTRIES = ("tt_gmm_fwd", "tt_gmm_dgrad", "tt_gmm_wgrad", "tt_gmm_fwd_gather",
                 "tt_gmm_dgrad_gather", "tt_gmm_wgrad_gather", "tt_gmm_fp8_fwd", "tt_gmm_fp8_dgrad")
 PERMUTE_ENTRIES = ("tt_permute_scatter", "tt_unpermute_gather")
+SWIGLU_ENTRIES = ("tt_swiglu_fwd", "tt_swiglu_bwd")
 ROUTER_ENTRIES = ("tt_router_gate_fwd", "tt_router_topk_fwd", "tt_router_topk_bwd",
                   "tt_router_loss_fwd", "tt_router_loss_bwd")
 
@@ -49,8 +50,10 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="qwen3_30b_a3b")
-    p.add_argument("--part", choices=("layer", "router"), default="layer",
-                   help="layer: the MoE layer step (default); router: the router front end only")
+    p.add_argument("--part", choices=("layer", "router", "dense-compare"), default="layer",
+                   help="layer: the MoE layer step (default); router: the router front end "
+                        "only; dense-compare: the workload's GEMM shapes as dense hipBLASLt "
+                        "products (torch.matmul) beside the grouped kernels at uniform loads")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -159,7 +162,7 @@ def gpu_run(w, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    timer = L.KernelTimer(GEMM_ENTRIES + PERMUTE_ENTRIES)
+    timer = L.KernelTimer(GEMM_ENTRIES + PERMUTE_ENTRIES + SWIGLU_ENTRIES)
     L.set_timer(timer)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -243,6 +246,54 @@ def router_line(w, args):
     }
 
 
+def dense_compare(w, reps):
+    """fc1 / fc2 of the workload as dense bf16 products through torch.matmul
+    (hipBLASLt) and the grouped kernels with every expert holding M / E rows,
+    the same flops: fwd y = x W, and the weight gradient x^T dy over all rows.
+    Median HIP-event time of ``reps`` launches each; for counter runs
+    (rocprofv3 tells the kernels apart by name)."""
+    import statistics
+
+    from torchturbo_amd import _lib as L
+
+    dev = torch.device("cuda", 0)
+    M, H, F, E = w.routed_rows, w.hidden, w.ffn, w.experts
+    g = torch.Generator(device=dev).manual_seed(1)
+    cnt = torch.full((E,), M // E, dtype=torch.int64, device=dev)
+    cnt[0] += M - int(cnt.sum())
+    st = L.stream(dev)
+    out = {}
+    for name, K, N in (("fc1", H, 2 * F), ("fc2", F, H)):
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        dy = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
+        wt = (torch.randn(E, K, N, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        dw = torch.empty_like(wt)
+        runs = {
+            "dense_fwd": lambda: torch.matmul(x, wt[0], out=y),
+            "dense_wgrad": lambda: torch.matmul(x.t(), dy),
+            "grouped_fwd": lambda: L.call("tt_gmm_fwd", L.ptr(x), L.ptr(wt), L.TT_BF16, M, K, N,
+                                          E, 0, L.ptr(cnt), L.ptr(y), st),
+            "grouped_wgrad": lambda: L.call("tt_gmm_wgrad", L.ptr(x), L.ptr(dy), L.TT_BF16, M, K,
+                                            N, E, 0, L.ptr(cnt), L.ptr(dw), st),
+        }
+        for kind, fn in runs.items():
+            fn()
+            torch.cuda.synchronize()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(reps)]
+            for a, b in ev:
+                a.record()
+                fn()
+                b.record()
+            torch.cuda.synchronize()
+            us = statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3
+            out[f"{name}_{kind}"] = {"us": round(us, 1),
+                                     "tflops": round(2.0 * M * K * N / us / 1e6, 1)}
+    return {"part": "dense-compare", "workload": w.name, "rows": M, "experts": E,
+            "shapes": {"fc1": [M, H, 2 * F], "fc2": [M, F, H]}, "results": out}
+
+
 def cpu_baseline(w, budget_s):
     """The CPU oracle (the reference's native composition) on a token sample."""
     from dataclasses import replace
@@ -312,6 +363,9 @@ def main():
     if args.part == "router":
         print(json.dumps(router_line(w, args)), flush=True)
         return
+    if args.part == "dense-compare":
+        print(json.dumps(dense_compare(w, max(args.steps, 1))), flush=True)
+        return
     ms, kernels = gpu_run(w, args.steps, args.warmup)
     tokens_per_s = w.tokens / (ms / 1e3)
 
@@ -327,6 +381,15 @@ def main():
     pass_bytes = w.permute_bytes()
     perm_gbs = pass_bytes / (perm_ms / 1e3 / perm_n) / 1e9 if perm_n else None
     unperm_gbs = pass_bytes / (unperm_ms / 1e3 / unperm_n) / 1e9 if unperm_n else None
+    # SwiGLU x probs: fwd reads [M, 2F] and the fp32 probs, writes [M, F]; bwd
+    # reads [M, 2F], [M, F] and the probs, writes [M, 2F] and fp32 d-probs.
+    M, F2, b = w.routed_rows, 2 * w.ffn, 2
+    sw_bytes = {"tt_swiglu_fwd": M * F2 * b + M * 4 + M * w.ffn * b,
+                "tt_swiglu_bwd": 2 * M * F2 * b + M * w.ffn * b + 8 * M}
+    sw_gbs = {}
+    for name, nbytes in sw_bytes.items():
+        n, t_ms = kernels.get(name, (0, 0.0))
+        sw_gbs[name] = round(nbytes / (t_ms / 1e3 / n) / 1e9, 1) if n else None
 
     line = {
         "metric": "MoE layer fwd+bwd tokens/sec on 1 MI355X; grouped-GEMM % MFMA peak",
@@ -367,6 +430,9 @@ def main():
             "permute_scatter_calls_per_step": perm_n / args.steps,
             "unpermute_gather_gbs": None if unperm_gbs is None else round(unperm_gbs, 1),
             "bytes_per_pass": pass_bytes,
+            "swiglu_fwd_gbs": sw_gbs["tt_swiglu_fwd"],
+            "swiglu_bwd_gbs": sw_gbs["tt_swiglu_bwd"],
+            "swiglu_bytes": sw_bytes,
         },
     }
     if not args.no_cpu_baseline:
