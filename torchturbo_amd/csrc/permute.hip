@@ -118,10 +118,13 @@ __global__ __launch_bounds__(256) void unpermute_gather_kernel(
 }
 
 // Same sum for top-k <= KMAX (small): every thread reads the token's row ids
-// (uniform loads), sorts them in registers, issues all K row loads before
-// adding, and accumulates in ascending row order. No block barrier, no LDS.
-// Row ids outside [0, M) contribute nothing (adding +0 to a sum that starts
-// at +0 leaves it unchanged, so skipping and adding zero agree bitwise).
+// (uniform loads), sorts them in registers, issues all K row loads of its NS
+// 16-byte column slices (v and v + blockDim.x) before adding, and
+// accumulates in ascending row order. No block barrier, no LDS. NS = 2 needs
+// the row's slice count to be a multiple of 2 * blockDim.x (the launch
+// checks it). Row ids outside [0, M) contribute nothing (adding +0 to a sum
+// that starts at +0 leaves it unchanged, so skipping and adding zero agree
+// bitwise).
 template <int DT>
 __device__ __forceinline__ float rnd_dt(float v) {
   if constexpr (DT == TT_BF16) return bf16_to_f32(f32_to_bf16(v));
@@ -137,7 +140,7 @@ __device__ __forceinline__ float load_w(const void* p, int64_t i) {
 
 constexpr int kNoProbs = -1;
 
-template <class TT, int XD, int PD, int V, int KMAX>
+template <class TT, int XD, int PD, int V, int KMAX, int NS>
 __global__ __launch_bounds__(1024) void unpermute_small_kernel(
     const typename TT::storage* __restrict__ packed, int64_t H, int K,
     const int32_t* __restrict__ rows, const int64_t* __restrict__ experts,
@@ -196,34 +199,42 @@ __global__ __launch_bounds__(1024) void unpermute_small_kernel(
   }
   // Rows are loaded unconditionally (an invalid row reads row 0 and counts
   // as zero): a load under a per-row branch would be waited for before the
-  // next one is issued. Each packed row is read once: streaming loads.
-  for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
-    St x[KMAX][V];
+  // next one is issued. Each packed row is read once: streaming loads. Two
+  // slices per thread keep 2 K loads in flight per thread (Qwen shape, 128
+  // threads: 2-3 % faster than one slice at 256 threads; four slices at 64
+  // threads lose occupancy and run 1.5x slower).
+  for (int64_t v = threadIdx.x; v < nv; v += NS * (int64_t)blockDim.x) {
+    St x[NS][KMAX][V];
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-      const int64_t r = rs[j] != 0x7fffffff ? rs[j] : 0;
-      load_stream<sizeof(x[j])>(x[j], packed + r * H + v * V);
-    }
-    float acc[V];
+    for (int u = 0; u < NS; ++u)
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-      const bool ok = rs[j] != 0x7fffffff;
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float xv = ok ? TT::to_f32(x[j][i]) : 0.0f;
-        if constexpr (PD != kNoProbs) acc[i] += rnd_dt<PR>(xv * ws[j]);
-        else acc[i] += xv;
+      for (int j = 0; j < KMAX; ++j) {
+        const int64_t r = rs[j] != 0x7fffffff ? rs[j] : 0;
+        load_stream<sizeof(x[u][j])>(x[u][j], packed + r * H + (v + u * (int64_t)blockDim.x) * V);
       }
-    }
-    St y[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) y[i] = TT::from_f32(rnd_dt<PR>(acc[i]));
-    // Streaming store: measured in the layer step, the token rows written
-    // this way leave the caches to the kernels that follow (Qwen unpermute
-    // 69 -> 72 % of HBM bandwidth, and the step faster).
-    store_stream<sizeof(y)>(out + t * H + v * V, y);
+    for (int u = 0; u < NS; ++u) {
+      float acc[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = 0.f;
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) {
+        const bool ok = rs[j] != 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const float xv = ok ? TT::to_f32(x[u][j][i]) : 0.0f;
+          if constexpr (PD != kNoProbs) acc[i] += rnd_dt<PR>(xv * ws[j]);
+          else acc[i] += xv;
+        }
+      }
+      St y[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) y[i] = TT::from_f32(rnd_dt<PR>(acc[i]));
+      // Streaming store: measured in the layer step, the token rows written
+      // this way leave the caches to the kernels that follow (Qwen unpermute
+      // 69 -> 72 % of HBM bandwidth, and the step faster).
+      store_stream<sizeof(y)>(out + t * H + (v + u * (int64_t)blockDim.x) * V, y);
+    }
   }
 }
 
@@ -402,26 +413,48 @@ int launch_unpermute(const void* packed, int64_t T, int64_t H, int K, const int3
   St* o = static_cast<St*>(out);
   if (al % 16 == 0 && K <= 8) {
     constexpr int V = 16 / sizeof(St);
-    // One thread per 16-byte column slice of the row, so that every thread
-    // issues all k row loads at once (H 4096: 512 threads).
     const int64_t nvb = H / V;
+    const dim3 grid((unsigned)T);
+    // Two 16-byte column slices per thread when they split the row exactly
+    // over 64-1024 threads (H 2048 bf16: 128 threads; 4096: 256; 7168: 448),
+    // else one slice per thread, so that every thread issues all of its row
+    // loads at once.
+    if (nvb % 128 == 0 && nvb / 2 <= 1024) {
+      const dim3 blk((unsigned)(nvb / 2));
+      if (probs == nullptr) {
+        if (K <= 2)
+          hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 2, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+        else
+          hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 8, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      } else if (pdt == TT_F32) {
+        if (K <= 2)
+          hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 2, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+        else
+          hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 8, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      } else if (pdt == TT_BF16) {
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_BF16, V, 8, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      } else {
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F16, V, 8, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      }
+      return tt_check_launch("unpermute_gather");
+    }
     const unsigned nthr =
         nvb <= 256 ? block_for(nvb) : (unsigned)(nvb <= 1024 ? ((nvb + 63) / 64) * 64 : 1024);
-    const dim3 grid((unsigned)T), blk(nthr);
+    const dim3 blk(nthr);
     if (probs == nullptr) {
       if (K <= 2)
-        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 2, 1>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
       else
-        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, kNoProbs, V, 8, 1>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
     } else if (pdt == TT_F32) {
       if (K <= 2)
-        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 2>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 2, 1>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
       else
-        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+        hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F32, V, 8, 1>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
     } else if (pdt == TT_BF16) {
-      hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_BF16, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_BF16, V, 8, 1>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
     } else {
-      hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F16, V, 8>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
+      hipLaunchKernelGGL((unpermute_small_kernel<TT, XD, TT_F16, V, 8, 1>), grid, blk, 0, s, p, H, K, rows, experts, probs, E, o, M);
     }
   } else if (al % 16 == 0) {
     constexpr int V = 16 / sizeof(St);
