@@ -250,8 +250,11 @@ def dense_compare(w, reps):
     """fc1 / fc2 of the workload as dense bf16 products through torch.matmul
     (hipBLASLt) and the grouped kernels with every expert holding M / E rows,
     the same flops: fwd y = x W, and the weight gradient x^T dy over all rows.
-    Median HIP-event time of ``reps`` launches each; for counter runs
-    (rocprofv3 tells the kernels apart by name)."""
+    The four launches of a shape alternate, back to back, ``reps`` times (a
+    launch's time depends on how long the chip has been under load, so
+    blocks of one kind would favour whichever ran first); median HIP-event
+    time of each kind. Also for counter runs (rocprofv3 tells the kernels
+    apart by name)."""
     import statistics
 
     from torchturbo_amd import _lib as L
@@ -269,25 +272,29 @@ def dense_compare(w, reps):
         wt = (torch.randn(E, K, N, generator=g, device=dev) * 0.02).to(torch.bfloat16)
         y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
         dw = torch.empty_like(wt)
+        dwd = torch.empty(K, N, dtype=torch.bfloat16, device=dev)
         runs = {
             "dense_fwd": lambda: torch.matmul(x, wt[0], out=y),
-            "dense_wgrad": lambda: torch.matmul(x.t(), dy),
+            "dense_wgrad": lambda: torch.matmul(x.t(), dy, out=dwd),
             "grouped_fwd": lambda: L.call("tt_gmm_fwd", L.ptr(x), L.ptr(wt), L.TT_BF16, M, K, N,
                                           E, 0, L.ptr(cnt), L.ptr(y), st),
             "grouped_wgrad": lambda: L.call("tt_gmm_wgrad", L.ptr(x), L.ptr(dy), L.TT_BF16, M, K,
                                             N, E, 0, L.ptr(cnt), L.ptr(dw), st),
         }
-        for kind, fn in runs.items():
+        for fn in runs.values():
             fn()
-            torch.cuda.synchronize()
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(reps)]
-            for a, b in ev:
+        torch.cuda.synchronize()
+        ev = {kind: [] for kind in runs}
+        for _ in range(reps):
+            for kind, fn in runs.items():
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 a.record()
                 fn()
                 b.record()
-            torch.cuda.synchronize()
-            us = statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3
+                ev[kind].append((a, b))
+        torch.cuda.synchronize()
+        for kind, pairs in ev.items():
+            us = statistics.median(a.elapsed_time(b) for a, b in pairs) * 1e3
             out[f"{name}_{kind}"] = {"us": round(us, 1),
                                      "tflops": round(2.0 * M * K * N / us / 1e6, 1)}
     return {"part": "dense-compare", "workload": w.name, "rows": M, "experts": E,
