@@ -18,6 +18,8 @@ oracle timed on a bounded sample of the same workload.
 ``--part router`` times the router front end instead: ``TopKRouter`` forward
 and backward on the workload's tokens (gating linear fused with the top-k,
 aux-loss and z-loss sums, 16-bit router weight, fp32 router dtype).
+``--part dense-compare`` times the workload's GEMM shapes through hipBLASLt
+beside the grouped kernels (see ``dense_compare``).
 """
 
 from __future__ import annotations
@@ -52,8 +54,9 @@ def parse():
     p.add_argument("--workload", default="qwen3_30b_a3b")
     p.add_argument("--part", choices=("layer", "router", "dense-compare"), default="layer",
                    help="layer: the MoE layer step (default); router: the router front end "
-                        "only; dense-compare: the workload's GEMM shapes as dense hipBLASLt "
-                        "products (torch.matmul) beside the grouped kernels at uniform loads")
+                        "only; dense-compare: the workload's GEMM shapes as dense and "
+                        "per-expert batched hipBLASLt products (torch.matmul / torch.bmm) "
+                        "beside the grouped kernels at uniform loads")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -247,14 +250,17 @@ def router_line(w, args):
 
 
 def dense_compare(w, reps):
-    """fc1 / fc2 of the workload as dense bf16 products through torch.matmul
-    (hipBLASLt) and the grouped kernels with every expert holding M / E rows,
-    the same flops: fwd y = x W, and the weight gradient x^T dy over all rows.
-    The four launches of a shape alternate, back to back, ``reps`` times (a
-    launch's time depends on how long the chip has been under load, so
-    blocks of one kind would favour whichever ran first); median HIP-event
-    time of each kind. Also for counter runs (rocprofv3 tells the kernels
-    apart by name)."""
+    """fc1 / fc2 of the workload through hipBLASLt (torch.matmul / torch.bmm,
+    bf16) beside the grouped kernels, with every expert holding M / E rows,
+    the same flops. dense: one product over all M rows (fwd y = x W with one
+    expert's weight; weight gradient x^T dy). batched: one product per expert
+    (fwd x_e W_e, weight gradient x_e^T dy_e, both operands contiguous), the
+    grouped problem with uniform loads, plus the transpose of x that the
+    batched weight gradient needs. The launches of a shape alternate,
+    back to back, ``reps`` times (a launch's time depends on how long the chip
+    has been under load, so blocks of one kind would favour whichever ran
+    first); median HIP-event time of each kind. Also for counter runs
+    (rocprofv3 tells the kernels apart by name)."""
     import statistics
 
     from torchturbo_amd import _lib as L
@@ -264,6 +270,7 @@ def dense_compare(w, reps):
     g = torch.Generator(device=dev).manual_seed(1)
     cnt = torch.full((E,), M // E, dtype=torch.int64, device=dev)
     cnt[0] += M - int(cnt.sum())
+    me = M // E
     st = L.stream(dev)
     out = {}
     for name, K, N in (("fc1", H, 2 * F), ("fc2", F, H)):
@@ -276,11 +283,19 @@ def dense_compare(w, reps):
         runs = {
             "dense_fwd": lambda: torch.matmul(x, wt[0], out=y),
             "dense_wgrad": lambda: torch.matmul(x.t(), dy, out=dwd),
-            "grouped_fwd": lambda: L.call("tt_gmm_fwd", L.ptr(x), L.ptr(wt), L.TT_BF16, M, K, N,
-                                          E, 0, L.ptr(cnt), L.ptr(y), st),
-            "grouped_wgrad": lambda: L.call("tt_gmm_wgrad", L.ptr(x), L.ptr(dy), L.TT_BF16, M, K,
-                                            N, E, 0, L.ptr(cnt), L.ptr(dw), st),
         }
+        if me * E == M:
+            # hipBLASLt's batched weight gradient takes x_e^T contiguous ([E, K, me]),
+            # a layout the layer does not hold: the transpose is timed on its own.
+            xt = x.view(E, me, K).transpose(1, 2).contiguous()
+            dwb = torch.empty_like(wt)
+            runs["batched_fwd"] = lambda: torch.bmm(x.view(E, me, K), wt, out=y.view(E, me, N))
+            runs["batched_wgrad"] = lambda: torch.bmm(xt, dy.view(E, me, N), out=dwb)
+            runs["transpose_x"] = lambda: xt.copy_(x.view(E, me, K).transpose(1, 2))
+        runs["grouped_fwd"] = lambda: L.call("tt_gmm_fwd", L.ptr(x), L.ptr(wt), L.TT_BF16, M, K,
+                                             N, E, 0, L.ptr(cnt), L.ptr(y), st)
+        runs["grouped_wgrad"] = lambda: L.call("tt_gmm_wgrad", L.ptr(x), L.ptr(dy), L.TT_BF16, M,
+                                               K, N, E, 0, L.ptr(cnt), L.ptr(dw), st)
         for fn in runs.values():
             fn()
         torch.cuda.synchronize()
@@ -295,8 +310,11 @@ def dense_compare(w, reps):
         torch.cuda.synchronize()
         for kind, pairs in ev.items():
             us = statistics.median(a.elapsed_time(b) for a, b in pairs) * 1e3
-            out[f"{name}_{kind}"] = {"us": round(us, 1),
-                                     "tflops": round(2.0 * M * K * N / us / 1e6, 1)}
+            out[f"{name}_{kind}"] = {"us": round(us, 1)}
+            if kind != "transpose_x":
+                out[f"{name}_{kind}"]["tflops"] = round(2.0 * M * K * N / us / 1e6, 1)
+        del runs, x, dy, wt, y, dw, dwd
+        torch.cuda.empty_cache()
     return {"part": "dense-compare", "workload": w.name, "rows": M, "experts": E,
             "shapes": {"fc1": [M, H, 2 * F], "fc2": [M, F, H]}, "results": out}
 
