@@ -301,6 +301,14 @@ int tt_gmm_wgrad_gather(const void* x, int64_t x_src_rows, const int32_t* x_src_
  * (e.g. more experts than their LDS schedule holds) keep the permutation. */
 int tt_gmm_gather_supported(int32_t op, int dtype, int64_t src_rows, int64_t m, int64_t k,
                             int64_t n, int32_t num_experts);
+/* Whether tt_gmm_wgrad runs this shape (bf16 / f16) on its persistent kernel
+ * (1) rather than the one-tile-per-block kernel (0), without launching: short
+ * reductions (m <= 512 * num_experts) or at least 32 output tiles of 256x256
+ * per expert. No counterpart in the reference: it reports the launcher's
+ * kernel choice, so that tests and tools can tell which kernel a shape
+ * exercises. */
+int tt_gmm_wgrad_persistent(int dtype, int64_t m, int64_t k, int64_t n, int32_t num_experts,
+                            int32_t trans_b);
 
 /* FP8 e4m3 weights with 128x128 block scales, HF [out, in] orientation:
  * qw [E, N, K] bytes, scale [E, ceil(N/128), ceil(K/128)] (bf16 or f32).

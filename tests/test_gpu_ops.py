@@ -1051,20 +1051,27 @@ def test_grouped_matmul_many_tiles(hip_ops, dtype, trans_b, E, M, K, N):
 
 
 @pytest.mark.parametrize("trans_b", [False, True])
-@pytest.mark.parametrize("E,K,N", [(64, 1024, 768), (13, 1024, 768), (13, 768, 768)])
+@pytest.mark.parametrize("E,K,N", [(64, 1024, 768), (13, 1024, 768), (13, 768, 768),
+                                   (16, 2048, 1024)])
 def test_grouped_matmul_long_wgrad_integer_exact(hip_ops, trans_b, E, K, N):
-    """Weight gradients with long expert reductions (mean load above 512 rows: the
-    four-stage kernel, one output tile per block) on small-integer operands, so every
-    sum is exact in fp32 and dW is the exact product rounded once. Zipf loads with
-    empty experts, a one-row expert and experts shorter than three 32-deep k-tiles.
-    With a 4 x 3 tile grid every expert's tiles go to one pair of XCDs (at E = 13, not a
-    multiple of 8, the blocks of ranks past the last expert exit); a 3 x 3 grid (no even
-    side) takes the all-XCD mapping."""
+    """Weight gradients with long expert reductions (mean load above 512 rows) on
+    small-integer operands, so every sum is exact in fp32 and dW is the exact product
+    rounded once. Zipf loads with empty experts, a one-row expert and experts shorter
+    than three 32-deep k-tiles. Below 32 output tiles per expert the four-stage kernel
+    takes them (one output tile per block): with a 4 x 3 tile grid every expert's tiles
+    go to one pair of XCDs (at E = 13, not a multiple of 8, the blocks of ranks past the
+    last expert exit); a 3 x 3 grid (no even side) takes the all-XCD mapping. An 8 x 4
+    grid takes the persistent kernel, whose longest reductions here run to 60 64-deep
+    k-tiles."""
     torch.backends.cuda.matmul.allow_tf32 = False
     counts = _zipf_counts(E, E * 1024, seed=5, empty=(3, 7) if E < 20 else (3, 17, 40))
     counts[11], counts[12] = 1, 70  # below three k-tiles
     counts[int(counts.argmax())] -= 71
     M = int(counts.sum())
+    from torchturbo_amd import _lib
+
+    tiles = -(-K // 256) * -(-N // 256)
+    assert _lib.load().tt_gmm_wgrad_persistent(_lib.TT_BF16, M, K, N, E, int(trans_b)) == (tiles >= 32)
     g = torch.Generator(device=DEV).manual_seed(3)
     x = torch.randint(-3, 4, (M, K), generator=g, device=DEV).to(torch.bfloat16)
     wshape = (E, N, K) if trans_b else (E, K, N)

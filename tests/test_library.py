@@ -77,3 +77,29 @@ def test_empty_problems_are_no_ops(lib):
     L.call("tt_router_topk_fwd", None, 0, 0, 8, 2, 0, 0, None, 0, 0, 0.0, None, None, None,
            None, None)
     L.call("tt_packed_probs_bwd", None, 0, 0, 2, 8, None, None, None, None)
+
+
+def test_shape_queries_answer_without_a_gpu(lib):
+    """The launch-choice queries are host arithmetic: the benchmark layers' shapes."""
+    bf = L.TT_BF16
+    wp = lib.tt_gmm_wgrad_persistent
+    # Qwen3 fc1 (48 output tiles per expert) and fc2 (24), 1024 rows per expert on average
+    assert wp(bf, 131072, 2048, 1536, 128, 0) == 1
+    assert wp(bf, 131072, 768, 2048, 128, 0) == 0
+    # short reductions (DeepSeek-V3: 128 rows per expert) and Mixtral's large grids
+    assert wp(bf, 32768, 7168, 4096, 256, 1) == 1
+    assert wp(bf, 32768, 2048, 7168, 256, 1) == 1
+    assert wp(bf, 16384, 4096, 28672, 8, 0) == 1
+    assert wp(bf, 16384, 14336, 4096, 8, 0) == 1
+    # fp32 takes its own kernel; invalid sizes are never persistent
+    assert wp(L.TT_F32, 131072, 2048, 1536, 128, 0) == 0
+    assert wp(bf, -1, 2048, 1536, 128, 0) == 0 and wp(bf, 1024, 2048, 1536, 0, 0) == 0
+    gs = lib.tt_gmm_gather_supported
+    # the Qwen3 layer's four gathering launches are taken; more experts than the LDS
+    # schedule holds are not; fp32 is not
+    assert gs(0, bf, 16384, 131072, 2048, 1536, 128) == 1
+    assert gs(1, bf, 16384, 131072, 768, 2048, 128) == 1
+    assert gs(2, bf, 16384, 131072, 2048, 1536, 128) == 1
+    assert gs(3, bf, 16384, 131072, 768, 2048, 128) == 1
+    assert gs(0, bf, 16384, 1048576, 2048, 1536, 1024) == 0
+    assert gs(0, L.TT_F32, 16384, 131072, 2048, 1536, 128) == 0

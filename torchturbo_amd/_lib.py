@@ -60,6 +60,7 @@ _PROTOS: dict[str, list] = {
     "tt_gmm_dgrad_gather": [P, I64, P, P, c_int, I64, I64, I64, I32, I32, P, P, P],
     "tt_gmm_wgrad_gather": [P, I64, P, P, I64, P, c_int, I64, I64, I64, I32, I32, P, P, P],
     "tt_gmm_gather_supported": [I32, c_int, I64, I64, I64, I64, I32],
+    "tt_gmm_wgrad_persistent": [c_int, I64, I64, I64, I32, I32],
     "tt_gmm_fp8_fwd": [P, P, P, c_int, I64, I64, I64, I32, P, P, P],
     "tt_gmm_fp8_dgrad": [P, P, P, c_int, I64, I64, I64, I32, P, P, P],
 }
