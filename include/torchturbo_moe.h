@@ -244,7 +244,8 @@ int tt_gated_act_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, int ac
  * grouped_gemm.ops.gmm (ops/providers/cuda/grouped_matmul.py:34-36).
  * dtype bf16/f16 (MFMA, fp32 accumulation) or f32.
  * Concurrency: weight-gradient launches that take the persistent kernel
- * (at most 512 rows per expert on average, M <= 512 * E) keep their work
+ * (at most 512 rows per expert on average, M <= 512 * E, or at least 32
+ * output tiles of 256x256 per expert; tt_gmm_wgrad_persistent) keep their work
  * queue in one of 64 slots of a per-process device array, taken in turn by
  * successive launches (each launch clears its slot on its stream first). At
  * most 64 such launches may be in flight at once across all streams of a
