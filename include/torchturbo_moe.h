@@ -243,14 +243,15 @@ int tt_gated_act_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, int ac
  * TorchGroupedMatmul (ops/providers/native/grouped_matmul.py:16-56) and
  * grouped_gemm.ops.gmm (ops/providers/cuda/grouped_matmul.py:34-36).
  * dtype bf16/f16 (MFMA, fp32 accumulation) or f32.
- * Concurrency: weight-gradient launches that take the persistent kernel
- * (at most 512 rows per expert on average, M <= 512 * E, or at least 32
- * output tiles of 256x256 per expert; tt_gmm_wgrad_persistent) keep their work
- * queue in one of 64 slots of a per-process device array, taken in turn by
- * successive launches (each launch clears its slot on its stream first). At
- * most 64 such launches may be in flight at once across all streams of a
- * device; launches on one stream never overlap, so a single stream has no
- * limit.
+ * Concurrency: every bf16 / f16 weight-gradient launch (tt_gmm_wgrad,
+ * tt_gmm_wgrad_gather) keeps per-launch state in one of 64 slots of a
+ * per-process device array, taken in turn by successive launches and written
+ * on the launch stream before the GEMM kernel runs: the persistent kernel's
+ * work queue (at most 512 rows per expert on average, M <= 512 * E, or at
+ * least 512 output tiles of 256x256 per expert; tt_gmm_wgrad_persistent), or
+ * the one-tile-per-block kernel's expert ranking. At most 64 weight-gradient
+ * launches may be in flight at once across all streams of a device; launches
+ * on one stream never overlap, so a single stream has no limit.
  * fwd:   y[M, N] = x[M, K] @ W[e] with W [E, K, N]; trans_b: W [E, N, K], W[e]^T. */
 int tt_gmm_fwd(const void* x, const void* w, int dtype, int64_t m, int64_t k, int64_t n,
                int32_t num_experts, int32_t trans_b, const int64_t* counts, void* y,
@@ -304,7 +305,7 @@ int tt_gmm_gather_supported(int32_t op, int dtype, int64_t src_rows, int64_t m, 
                             int64_t n, int32_t num_experts);
 /* Whether tt_gmm_wgrad runs this shape (bf16 / f16) on its persistent kernel
  * (1) rather than the one-tile-per-block kernel (0), without launching: short
- * reductions (m <= 512 * num_experts) or at least 32 output tiles of 256x256
+ * reductions (m <= 512 * num_experts) or at least 512 output tiles of 256x256
  * per expert. No counterpart in the reference: it reports the launcher's
  * kernel choice, so that tests and tools can tell which kernel a shape
  * exercises. */

@@ -1052,16 +1052,17 @@ def test_grouped_matmul_many_tiles(hip_ops, dtype, trans_b, E, M, K, N):
 
 @pytest.mark.parametrize("trans_b", [False, True])
 @pytest.mark.parametrize("E,K,N", [(64, 1024, 768), (13, 1024, 768), (13, 768, 768),
-                                   (16, 2048, 1024)])
+                                   (16, 2048, 1024), (13, 2048, 16384)])
 def test_grouped_matmul_long_wgrad_integer_exact(hip_ops, trans_b, E, K, N):
     """Weight gradients with long expert reductions (mean load above 512 rows) on
     small-integer operands, so every sum is exact in fp32 and dW is the exact product
     rounded once. Zipf loads with empty experts, a one-row expert and experts shorter
-    than three 32-deep k-tiles. Below 32 output tiles per expert the four-stage kernel
-    takes them (one output tile per block): with a 4 x 3 tile grid every expert's tiles
-    go to one pair of XCDs (at E = 13, not a multiple of 8, the blocks of ranks past the
-    last expert exit); a 3 x 3 grid (no even side) takes the all-XCD mapping. An 8 x 4
-    grid takes the persistent kernel, whose longest reductions here run to 60 64-deep
+    than three 32-deep k-tiles. Below 512 output tiles per expert the four-stage kernel
+    takes them (one output tile per block, experts in the longest-first order of the
+    launch's ranking): with a 4 x 3 or 8 x 4 tile grid every expert's tiles go to one
+    pair of XCDs (at E = 13, not a multiple of 8, the blocks of ranks past the last
+    expert exit); a 3 x 3 grid (no even side) takes the all-XCD mapping. An 8 x 64 grid
+    takes the persistent kernel, whose longest reduction here runs to 91 64-deep
     k-tiles."""
     torch.backends.cuda.matmul.allow_tf32 = False
     counts = _zipf_counts(E, E * 1024, seed=5, empty=(3, 7) if E < 20 else (3, 17, 40))
@@ -1071,7 +1072,7 @@ def test_grouped_matmul_long_wgrad_integer_exact(hip_ops, trans_b, E, K, N):
     from torchturbo_amd import _lib
 
     tiles = -(-K // 256) * -(-N // 256)
-    assert _lib.load().tt_gmm_wgrad_persistent(_lib.TT_BF16, M, K, N, E, int(trans_b)) == (tiles >= 32)
+    assert _lib.load().tt_gmm_wgrad_persistent(_lib.TT_BF16, M, K, N, E, int(trans_b)) == (tiles >= 512)
     g = torch.Generator(device=DEV).manual_seed(3)
     x = torch.randint(-3, 4, (M, K), generator=g, device=DEV).to(torch.bfloat16)
     wshape = (E, N, K) if trans_b else (E, K, N)
@@ -1087,6 +1088,39 @@ def test_grouped_matmul_long_wgrad_integer_exact(hip_ops, trans_b, E, K, N):
             dwe = xs[e].t() @ ds[e]  # [K, N], exact (integer sums below 2^24)
             ref = (dwe.t() if trans_b else dwe).to(torch.bfloat16)
             assert torch.equal(w.grad[e], ref), (e, int(counts[e]))
+
+
+def test_grouped_matmul_wgrad_ranking_many_experts_exact(hip_ops):
+    """The one-tile-per-block weight gradient takes experts longest first from a ranking
+    computed once per launch (one thread per expert, a block per 256 experts). 300
+    experts: a run of 80 equal loads (ranked by id), empty and one-row experts and one
+    long expert, small-integer operands so dW is exact. A rank written twice or not at
+    all would leave an expert's gradient unwritten or written from another's rows."""
+    from torchturbo_amd import _lib
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    E, K, N = 300, 256, 512
+    counts = torch.full((E,), 720, dtype=torch.int64)
+    counts[::7] = 0
+    counts[5::11] = 1
+    counts[100:180] = 900
+    counts[299] = 5000
+    M = int(counts.sum())
+    assert M > 512 * E
+    assert _lib.load().tt_gmm_wgrad_persistent(_lib.TT_BF16, M, K, N, E, 0) == 0
+    g = torch.Generator(device=DEV).manual_seed(11)
+    x = torch.randint(-3, 4, (M, K), generator=g, device=DEV).to(torch.bfloat16)
+    w = torch.randint(-3, 4, (E, K, N), generator=g, device=DEV).to(torch.bfloat16)
+    w.requires_grad_()
+    dy = torch.randint(-3, 4, (M, N), generator=g, device=DEV).to(torch.bfloat16)
+    xs = torch.split(x.float(), counts.tolist())
+    ds = torch.split(dy.float(), counts.tolist())
+    ref = torch.stack([(a.t() @ b).to(torch.bfloat16) for a, b in zip(xs, ds)])
+    for _ in range(2):  # twice: the second launch ranks into another slot
+        w.grad = None
+        y = hip_ops.grouped_matmul(x, w, counts.to(DEV))
+        y.backward(dy)
+        assert torch.equal(w.grad, ref)
 
 
 # ---------------------------------------------------------------------------

@@ -84,8 +84,12 @@ def test_shape_queries_answer_without_a_gpu(lib):
     bf = L.TT_BF16
     wp = lib.tt_gmm_wgrad_persistent
     # Qwen3 fc1 (48 output tiles per expert) and fc2 (24), 1024 rows per expert on average
-    assert wp(bf, 131072, 2048, 1536, 128, 0) == 1
+    assert wp(bf, 131072, 2048, 1536, 128, 0) == 0
     assert wp(bf, 131072, 768, 2048, 128, 0) == 0
+    # the boundary: 16 x 32 tiles per expert are persistent, 16 x 31 are not
+    assert wp(bf, 8192, 4096, 8192, 8, 0) == 1
+    assert wp(bf, 8192, 4096, 7936, 8, 0) == 0
+    assert wp(bf, 8192, 8192, 4096, 8, 1) == 1
     # short reductions (DeepSeek-V3: 128 rows per expert) and Mixtral's large grids
     assert wp(bf, 32768, 7168, 4096, 256, 1) == 1
     assert wp(bf, 32768, 2048, 7168, 256, 1) == 1

@@ -201,14 +201,61 @@ __host__ __device__ inline int wgrad_pair_split(int tiles_i, int tiles_j) {
   return ej ? 2 : 0;
 }
 
+// Weight-gradient launches own one of WQ_SLOTS slots of per-process device
+// state (slots rotate between launches): the persistent kernel's ticket
+// counters, or the one-tile-per-block kernel's expert ranking.
+constexpr int WQ_SLOTS = 64;
+
+// Expert ranking of a one-tile-per-block weight-gradient launch, computed once
+// per launch by wgrad_rank_kernel on the launch stream: entry r of the slot is
+// the expert of rank r, longest first (row count descending, ties by id), with
+// its first row and row count. Without it every block would scan the counts
+// and rank all experts itself, about 9.5k cycles per block against 4.5-4.8k
+// for a median k-loop of Qwen3-30B-A3B's gathered weight gradients (stamped
+// per block: 12.6 % of the CUs' time).
+struct WgradRank {
+  int64_t seg0;
+  int32_t nrows;
+  int32_t e;
+};
+constexpr int WR_MAX_E = 4096;
+__device__ WgradRank g_wgrad_rank[WQ_SLOTS * WR_MAX_E];
+
+// One thread per expert (grid ceil(E / 256)); each block scans all the counts
+// and ranks its experts against all of them. Counts sum to at most M < 2^31
+// rows (the launchers' 32-bit offset limits), so they compare as int.
+__global__ __launch_bounds__(256) void wgrad_rank_kernel(const int64_t* __restrict__ counts, int E,
+                                                         int slot) {
+  __shared__ int64_t row_start[WR_MAX_E + 1];
+  __shared__ int tile_start[WR_MAX_E + 1];
+  __shared__ int cnt[WR_MAX_E];
+  scan_counts<256>(counts, E, 1, row_start, tile_start);
+  for (int x = threadIdx.x; x < E; x += 256) cnt[x] = (int)(row_start[x + 1] - row_start[x]);
+  __syncthreads();
+  const int x = blockIdx.x * 256 + threadIdx.x;
+  if (x >= E) return;
+  const int cx = cnt[x];
+  int r = 0;
+#pragma unroll 8
+  for (int y = 0; y < E; ++y) {
+    const int cy = cnt[y];
+    r += (cy > cx) | ((cy == cx) & (y < x));
+  }
+  g_wgrad_rank[slot * WR_MAX_E + r] = WgradRank{row_start[x], cx, x};
+}
+
 // PAIRS: weight-gradient tiles on XCD pairs (wgrad_pair_split); the launch
 // must then size the grid as 8 ceil(E / 8) x tiles_i x tiles_j.
+// RSLOT (weight gradients): slot of the launch's expert ranking
+// (wgrad_rank_kernel), or -1 to scan and rank in the block.
 template <int NT, int BM, int BN, int MODE, bool TRANS_B, int ESZ, int WSZ, bool PAIRS = false>
 __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t K, int64_t N,
                               int E, const int64_t* __restrict__ counts, int tiles_i, int tiles_j,
-                              int64_t* row_start, int* tile_start, TileDesc& t) {
-  scan_counts<NT>(counts, E, BM, row_start, tile_start);
+                              int64_t* row_start, int* tile_start, TileDesc& t, int rslot = -1) {
+  const bool ranked = MODE == MODE_WGRAD && rslot >= 0;
+  if (!ranked) scan_counts<NT>(counts, E, BM, row_start, tile_start);
   int e, it, jt;
+  int64_t seg0 = 0, nrows = 0;
   if constexpr (MODE == MODE_WGRAD) {
     // Experts are taken longest first (rank by row count, ties by id) so the
     // long reductions of heavily loaded experts start early.
@@ -257,33 +304,44 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
       jt = rem % tiles_j;
     }
     if (rank >= E) return false;
-    // Rank of every expert, its comparisons split over NT / E threads per
-    // expert and summed with LDS atomics; int32 counts after the schedule.
-    int* cnt = tile_start + E + 1;
-    int* rnk = cnt + E;
-    for (int x = threadIdx.x; x < E; x += NT) {
-      cnt[x] = (int)(row_start[x + 1] - row_start[x]);
-      rnk[x] = 0;
-    }
-    __syncthreads();
-    const int parts = E >= NT ? 1 : NT / E;
-    for (int idx = threadIdx.x; idx < E * parts; idx += NT) {
-      const int x = idx % E, part = idx / E;
-      const int y0 = part * E / parts, y1 = (part + 1) * E / parts;
-      const int cx = cnt[x];
-      int r = 0;
-#pragma unroll 8
-      for (int y = y0; y < y1; ++y) {
-        const int cy = cnt[y];
-        r += (cy > cx) | ((cy == cx) & (y < x));
+    if (ranked) {
+      // One scalar load: the ranking was written by the kernel before this
+      // one on the launch stream.
+      const WgradRank w = g_wgrad_rank[rslot * WR_MAX_E + rank];
+      e = w.e;
+      seg0 = w.seg0;
+      nrows = w.nrows;
+    } else {
+      // Rank of every expert, its comparisons split over NT / E threads per
+      // expert and summed with LDS atomics; int32 counts after the schedule.
+      int* cnt = tile_start + E + 1;
+      int* rnk = cnt + E;
+      for (int x = threadIdx.x; x < E; x += NT) {
+        cnt[x] = (int)(row_start[x + 1] - row_start[x]);
+        rnk[x] = 0;
       }
-      atomicAdd(&rnk[x], r);
+      __syncthreads();
+      const int parts = E >= NT ? 1 : NT / E;
+      for (int idx = threadIdx.x; idx < E * parts; idx += NT) {
+        const int x = idx % E, part = idx / E;
+        const int y0 = part * E / parts, y1 = (part + 1) * E / parts;
+        const int cx = cnt[x];
+        int r = 0;
+#pragma unroll 8
+        for (int y = y0; y < y1; ++y) {
+          const int cy = cnt[y];
+          r += (cy > cx) | ((cy == cx) & (y < x));
+        }
+        atomicAdd(&rnk[x], r);
+      }
+      __syncthreads();
+      for (int x = threadIdx.x; x < E; x += NT)
+        if (rnk[x] == rank) lpt_expert = x;
+      __syncthreads();
+      e = lpt_expert;
+      seg0 = row_start[e];
+      nrows = row_start[e + 1] - seg0;
     }
-    __syncthreads();
-    for (int x = threadIdx.x; x < E; x += NT)
-      if (rnk[x] == rank) lpt_expert = x;
-    __syncthreads();
-    e = lpt_expert;
   } else {
     const int lb = xcd_remap(blockIdx.x, gridDim.x);
     const int slot = lb / tiles_j;
@@ -296,10 +354,12 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
     }
     e = lo;
     it = slot - tile_start[e];
+    seg0 = row_start[e];
+    nrows = row_start[e + 1] - seg0;
   }
   t.e = e;
-  t.seg0 = row_start[e];
-  t.nrows = row_start[e + 1] - t.seg0;
+  t.seg0 = seg0;
+  t.nrows = nrows;
   if constexpr (MODE == MODE_FWD) {
     t.a = p0 + t.seg0 * K * ESZ; t.lda = K;
     t.b = p1 + (int64_t)e * K * N * WSZ; t.ldb = TRANS_B ? K : N;
@@ -524,7 +584,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
                                                          const int64_t* __restrict__ counts,
                                                          int tiles_i, int tiles_j,
                                                          const int32_t* __restrict__ grow,
-                                                         int64_t gsrc_rows) {
+                                                         int64_t gsrc_rows, int rslot) {
   typedef Layout<MODE, TRANS_B> Lay;
   constexpr int WT = 128, FM = 4, FN = 4;
   constexpr bool GATH = GX != 0;
@@ -545,7 +605,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   TileDesc t;
   if (!describe_tile<DM_NT, DM_BM, DM_BN, MODE, TRANS_B, 2, 2, true>(p0, p1, out, K, N, E, counts,
                                                                  tiles_i, tiles_j, row_start,
-                                                                 tile_start, t))
+                                                                 tile_start, t, rslot))
     return;
 
   const int lane = threadIdx.x & 63;
@@ -870,7 +930,7 @@ constexpr int P_EPI = 4096;             // epilogue staging per wave
 // this (a handful of 64-deep k-tiles per output tile).
 constexpr int64_t P_WGRAD_ROWS = 512;
 // ... or experts of at least this many 256x256 output tiles.
-constexpr int P_WGRAD_TILES = 32;
+constexpr int P_WGRAD_TILES = 512;
 
 // K-major 64-deep tile: LDS row r (128 bytes) holds tile row r, its 16-byte
 // chunk c in slot c ^ ((r >> 1) & 7): any 16 consecutive rows then cover the
@@ -980,7 +1040,7 @@ __device__ __forceinline__ void store_wave_tile_p64(const f32x16 (&acc)[4][4], c
 // the launch stream just before the launch. Blocks take tickets with atomic
 // adds and leave once a ticket passes the end of their class's list; no block
 // ever waits for another.
-constexpr int WQ_SLOTS = 64, WQ_CLASSES = 8, WQ_STRIDE = 16;
+constexpr int WQ_CLASSES = 8, WQ_STRIDE = 16;
 __device__ int g_wgrad_queue[WQ_SLOTS * WQ_STRIDE];
 
 __global__ void wgrad_queue_reset_kernel(int slot) {
@@ -2382,6 +2442,13 @@ int allow_lds(F* kernel, size_t lds, size_t& allowed) {
   return TT_OK;
 }
 
+// Slot of the next weight-gradient launch (either kernel), in turn over all
+// launches of the process.
+int next_wgrad_slot() {
+  static std::atomic<unsigned> next{0};
+  return (int)(next.fetch_add(1, std::memory_order_relaxed) % WQ_SLOTS);
+}
+
 template <int MODE, bool TB, int ET, bool KMASK, int GX = 0>
 int launch_mfma_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K, int64_t N,
                   int E, const int64_t* counts, hipStream_t s, int64_t nblk, int ti, int tj,
@@ -2390,14 +2457,24 @@ int launch_mfma_k(const void* p0, const void* p1, void* out, int64_t M, int64_t 
   // ranks and tile (see describe_tile).
   if (MODE == MODE_WGRAD && wgrad_pair_split(ti, tj) != 0)
     nblk = 8 * (int64_t)((E + 7) / 8) * ti * tj;
-  const size_t lds = schedule_bytes(E);  // the stages are static LDS
+  // Weight gradients: the expert ranking once per launch, into a slot of its
+  // own, on the launch stream; the blocks then need no schedule in LDS.
+  int rslot = -1;
+  if (MODE == MODE_WGRAD && E <= WR_MAX_E) {
+    rslot = next_wgrad_slot();
+    hipLaunchKernelGGL(wgrad_rank_kernel, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, s,
+                       counts, E, rslot);
+    const int rr = tt_check_launch("gmm");
+    if (rr != TT_OK) return rr;
+  }
+  const size_t lds = rslot >= 0 ? 0 : schedule_bytes(E);  // the stages are static LDS
   static size_t allowed = 64 * 1024;
   const int rc = allow_lds(&gmm_mfma_kernel<MODE, TB, ET, KMASK, GX>, lds, allowed);
   if (rc != TT_OK) return rc;
   hipLaunchKernelGGL((gmm_mfma_kernel<MODE, TB, ET, KMASK, GX>), dim3((unsigned)nblk),
                      dim3(DM_NT), lds, s, static_cast<const char*>(p0),
                      static_cast<const char*>(p1), static_cast<char*>(out), M, K, N, E, counts,
-                     ti, tj, grow, gsrc_rows);
+                     ti, tj, grow, gsrc_rows, rslot);
   return tt_check_launch("gmm");
 }
 
@@ -2428,9 +2505,11 @@ size_t p64_schedule_bytes(int E) { return schedule_bytes(E) + (size_t)E * sizeof
 // operand panels and overlaps each tile's epilogue with the next tile's
 // loads, while the one-tile-per-block kernel keeps an expert's tiles on one
 // pair of XCDs, which pays for smaller tile grids. Measured on packed
-// operands with the layers' own routing (bit-identical either way): Qwen3 fc1
-// (48 tiles per expert) 831 against 907 us, Mixtral fc1 / fc2 (1792 / 896)
-// 3486 / 1625 against 3748 / 1681 us, Qwen3 fc2 (24) 499 against 469 us.
+// operands with the layers' own routing, launches alternated (bit-identical
+// either way), persistent against one tile per block: Mixtral fc1 (1792
+// tiles per expert) 3519 against 3650 us, fc2 (896) 1676 against 1663 us;
+// Qwen3-30B-A3B fc1 (48) 860 against 842 us, fc2 (24) 516 against 443 us;
+// the varlen stress layer's fc1 (48) 3276 against 2974 us.
 bool wgrad_persistent(int64_t M, int64_t K, int64_t N, int E, int ti, int tj) {
   const int64_t ld = K > N ? K : N;
   return (M <= (int64_t)E * P_WGRAD_ROWS || (int64_t)ti * tj >= P_WGRAD_TILES) &&
@@ -2449,8 +2528,7 @@ int launch_p64_k(const void* p0, const void* p1, void* out, int64_t M, int64_t K
   int slot = 0;
   if constexpr (MODE == MODE_WGRAD) {
     // A queue slot of its own for this launch, zeroed on the launch stream.
-    static std::atomic<unsigned> next_slot{0};
-    slot = (int)(next_slot.fetch_add(1, std::memory_order_relaxed) % WQ_SLOTS);
+    slot = next_wgrad_slot();
     hipLaunchKernelGGL(wgrad_queue_reset_kernel, dim3(1), dim3(64), 0, s, slot);
     const int rq = tt_check_launch("gmm");
     if (rq != TT_OK) return rq;
