@@ -288,8 +288,9 @@ int tt_gmm_dgrad_gather(const void* dy_src, int64_t src_rows, const int32_t* src
  * non-NULL; the other operand is packed [m, k] / [m, n]): x_src
  * [x_src_rows, k] or dy_src [dy_src_rows, n]. Equals tt_gmm_wgrad on the
  * gathered rows bit for bit. Long expert reductions only (m > 512 *
- * num_experts, the four-stage kernel); other problems return
- * TT_ERR_INVALID. */
+ * num_experts, the four-stage kernel), bf16 / f16, a source of fewer than
+ * 2^24 rows of fewer than 2^23 elements and under 4 GiB (its row offsets
+ * are 24-bit products); other problems return TT_ERR_INVALID. */
 int tt_gmm_wgrad_gather(const void* x, int64_t x_src_rows, const int32_t* x_src_of_row,
                         const void* dy, int64_t dy_src_rows, const int32_t* dy_src_of_row,
                         int dtype, int64_t m, int64_t k, int64_t n, int32_t num_experts,

@@ -107,3 +107,6 @@ def test_shape_queries_answer_without_a_gpu(lib):
     assert gs(3, bf, 16384, 131072, 768, 2048, 128) == 1
     assert gs(0, bf, 16384, 1048576, 2048, 1536, 1024) == 0
     assert gs(0, L.TT_F32, 16384, 131072, 2048, 1536, 128) == 0
+    # gathering weight gradients take sources of fewer than 2^24 rows (24-bit offsets)
+    assert gs(2, bf, (1 << 24) - 1, 1 << 24, 64, 64, 8) == 1
+    assert gs(2, bf, 1 << 24, 1 << 24, 64, 64, 8) == 0

@@ -187,6 +187,13 @@ struct TileDesc {
   int nsub;  // persistent fwd / dgrad: thin tiles in this slot (0: one ordinary tile)
 };
 
+// A block-uniform 64-bit value (read from LDS) into scalar registers.
+__device__ __forceinline__ int64_t rfl64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Weight-gradient tiles of one block per tile (gmm_mfma_kernel): each
 // expert's output tiles go to one pair of XCDs, half of its tile grid to
 // each, so an XCD's blocks re-read an expert's activation panels from L2
@@ -357,9 +364,14 @@ __device__ bool describe_tile(const char* p0, const char* p1, char* out, int64_t
     seg0 = row_start[e];
     nrows = row_start[e + 1] - seg0;
   }
-  t.e = e;
-  t.seg0 = seg0;
-  t.nrows = nrows;
+  // Block-uniform (some of it was read from LDS): scalar registers, so that
+  // resources and loop bounds derived from it stay scalar.
+  t.e = __builtin_amdgcn_readfirstlane(e);
+  t.seg0 = rfl64(seg0);
+  t.nrows = rfl64(nrows);
+  it = __builtin_amdgcn_readfirstlane(it);
+  jt = __builtin_amdgcn_readfirstlane(jt);
+  e = t.e;
   if constexpr (MODE == MODE_FWD) {
     t.a = p0 + t.seg0 * K * ESZ; t.lda = K;
     t.b = p1 + (int64_t)e * K * N * WSZ; t.ldb = TRANS_B ? K : N;
@@ -432,6 +444,23 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, int64_t bytes) {
 // compiler does not drain outstanding loads before every LDS read:
 // completion of a stage is awaited explicitly (TT_WAIT_VMCNT) before the
 // barrier that publishes it. Nothing else in these kernels uses M0.
+// The resource moved `adv` bytes along (scalar arithmetic): an offset from
+// the new base is in range exactly when the same offset plus adv was before,
+// and nothing is once adv passes the end.
+__device__ __forceinline__ i32x4 advance_rsrc(i32x4 r, uint32_t adv) {
+  const uint64_t b = (((uint64_t)(uint32_t)r.y << 32) | (uint32_t)r.x) + adv;  // stride 0
+  i32x4 o;
+  o.x = (int)(uint32_t)b;
+  o.y = (int)(uint32_t)(b >> 32);
+  // records - adv, or 0 on a borrow (SCC), in scalar instructions: the
+  // compiler's saturating subtract is a vector one.
+  uint32_t n;
+  asm("s_sub_u32 %0, %1, %2\n\ts_cselect_b32 %0, 0, %0" : "=s"(n) : "s"(r.z), "s"(adv) : "scc");
+  o.z = (int)n;
+  o.w = r.w;
+  return o;
+}
+
 __device__ __forceinline__ void dma16(uint32_t voff, i32x4 rsrc, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
@@ -665,7 +694,11 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   // them, was 4-16 % slower): each chunk's offset is its source row's plus
   // the lane's column chunk (two, by k-row parity). Reduction rows past the
   // expert's end read as zeros.
+  // gof: the chunks' offsets; fixed (the k-tile's advance is in the resource)
+  // except for the gathered operand's waves, which set them per k-tile.
   uint32_t grow_v[8], gof[8], gcol[2];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) gof[q] = voff[q];
   const uint32_t ld2 = (uint32_t)(ld * 2);
   const i32x4 irsrc = make_rsrc(grow, GATH ? M * 4 : 0);
   if constexpr (GATH) {
@@ -682,41 +715,55 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
          lds_addr_of((lds_char*)gidx) + (uint32_t)((wv * 2 + (grp & 1)) * 256));
   };
   const uint32_t gsrc = (uint32_t)gsrc_rows;
+  // An entry outside [0, gsrc_rows) (a negative one reads as a large
+  // unsigned value) becomes gsrc_rows: its offset lies past the source's
+  // resource, so it reads a row of zeros (the launch bounds
+  // (gsrc_rows + 1) * ld * 2 below 4 GiB, so the offset does not wrap, and
+  // gsrc_rows and ld * 2 below 2^24, so the product takes the 24-bit
+  // multiply-add). Only an expert's last k-tile has rows past its end.
   auto offsets = [&](int kk) {  // byte offsets of k-tile kk's chunks from its rows
+    if ((kk + 1) * DM_BK <= kvalid) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int row = kk * DM_BK + 2 * (wv * 8 + q) + (lane >> 5);
-      gof[q] = row < kvalid ? grow_v[q] * ld2 + gcol[q & 1] : DM_OOB;
+      for (int q = 0; q < 8; ++q)
+        gof[q] = (uint32_t)__umul24(min(grow_v[q], gsrc), ld2) + gcol[q & 1];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int row = kk * DM_BK + 2 * (wv * 8 + q) + (lane >> 5);
+        gof[q] = row < kvalid ? (uint32_t)__umul24(min(grow_v[q], gsrc), ld2) + gcol[q & 1]
+                              : DM_OOB;
+      }
     }
   };
   auto read_rows = [&](int kk) {  // source rows of k-tile kk's eight chunks
     lds_char* const ring = (lds_char*)gidx + (wv * 2 + ((kk >> 2) & 1)) * 256;
     const uint32_t at = (uint32_t)(((kk & 3) * 16 + (lane >> 5) * 8) * 4);
     const uint4 i0 = read_k(ring, at), i1 = read_k(ring, at + 16);
-    // An entry outside [0, gsrc_rows) (a negative one reads as a large
-    // unsigned value) becomes gsrc_rows: its offset lies past the source's
-    // resource, so it reads a row of zeros (the launch bounds
-    // (gsrc_rows + 1) * ld * 2 below 4 GiB, so the offset does not wrap).
-    grow_v[0] = min(i0.x, gsrc); grow_v[1] = min(i0.y, gsrc);
-    grow_v[2] = min(i0.z, gsrc); grow_v[3] = min(i0.w, gsrc);
-    grow_v[4] = min(i1.x, gsrc); grow_v[5] = min(i1.y, gsrc);
-    grow_v[6] = min(i1.z, gsrc); grow_v[7] = min(i1.w, gsrc);
+    grow_v[0] = i0.x; grow_v[1] = i0.y; grow_v[2] = i0.z; grow_v[3] = i0.w;
+    grow_v[4] = i1.x; grow_v[5] = i1.y; grow_v[6] = i1.z; grow_v[7] = i1.w;
   };
 
-  // Chunk q of k-tile kt into stage `stg`.
-  auto issue_one = [&](lds_char* stg, int kt, int q) {
-    uint32_t off = voff[q] + (uint32_t)kt * kstep;
+  // The resource of k-tile kt's loads: advanced by kt k-tiles (the chunk
+  // offsets stay fixed, so a load needs no vector arithmetic), or the whole
+  // source for the gathered operand (its offsets are absolute).
+  auto tile_rsrc = [&](int kt) -> i32x4 {
+    if constexpr (GATH) {
+      if (gath) return rsrc;
+    }
+    return advance_rsrc(rsrc, (uint32_t)kt * kstep);
+  };
+  // Chunk q of k-tile kt into stage `stg` through rr = tile_rsrc(kt).
+  auto issue_one = [&](lds_char* stg, const i32x4& rr, int kt, int q) {
+    uint32_t off = gof[q];
     if constexpr (KMASK) {
       if (kmaj && kt * DM_BK + kof[q] >= kvalid) off = DM_OOB;
     }
-    if constexpr (GATH) {
-      if (gath) off = gof[q];
-    }
-    dma16(off, rsrc, lds_addr_of(stg) + dst_wave + (uint32_t)q * 1024u);
+    dma16(off, rr, lds_addr_of(stg) + dst_wave + (uint32_t)q * 1024u);
   };
   auto issue = [&](lds_char* stg, int kt) {
+    const i32x4 rr = tile_rsrc(kt);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) issue_one(stg, kt, q);
+    for (int q = 0; q < 8; ++q) issue_one(stg, rr, kt, q);
   };
 
   // Fragment read offsets (K-major: per k-step; MN-major: per 32-wide block).
@@ -796,11 +843,12 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
       }
     }
     refresh();
+    const i32x4 rr = tile_rsrc(kt + 3);
 #pragma unroll
     for (int i = 0; i < FM * FN; ++i) {
       mfma(i, a1, b1);
       if (i < FM + FN) frag(nxt, 0, i, a0, b0);
-      if (i < 8) issue_one(refill, kt + 3, i);
+      if ((i & 1) == 0) issue_one(refill, rr, kt + 3, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -853,12 +901,6 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
 // compiler from moving LDS accesses across it. Loads in flight (vmcnt) are
 // not waited for.
 #define TT_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
-
-__device__ __forceinline__ int64_t rfl64(int64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
 
 // Output tile L (fwd / dgrad) from the schedule in LDS.
 template <int MODE, bool TRANS_B, int ESZ>
@@ -2614,6 +2656,8 @@ const char* wgrad_gather_limit(int GX, int64_t src_rows, int64_t M, int64_t K, i
   const int64_t gld = GX == 1 ? K : N;
   if (!(src_rows >= 1 && (src_rows + 1) * gld * 2 < (int64_t)DM_OOB))
     return "the source must hold at least one row and less than 4 GiB";
+  if (!(src_rows < (1 << 24) && gld * 2 < (1 << 24)))
+    return "the source must hold fewer than 2^24 rows of fewer than 2^23 elements";
   return nullptr;
 }
 
