@@ -618,9 +618,11 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   constexpr int WT = 128, FM = 4, FN = 4;
   constexpr bool GATH = GX != 0;
   static_assert(!GATH || (MODE == MODE_WGRAD && !KMASK), "gathered rows: weight gradients only");
-  // Gathered operand: per wave, two groups of four k-tiles of source row
-  // indices (lane i of a group: k-tile i / 16, k-row 2 (8 wv + i % 8) + i / 8 % 2).
-  __shared__ __align__(16) int gidx[GATH ? 2 * 2 * 64 : 4];
+  // Gathered operand: per wave, two groups of eight k-tiles of source row
+  // indices, 64 each (lane i of a group: k-tile i / 8, k-row
+  // 8 wave + 2 (i % 4) + i / 4 % 2, so a lane's four rows of a k-tile are one
+  // 16-byte read).
+  __shared__ __align__(16) int gidx[GATH ? 4 * 2 * 64 : 4];
   // One static LDS array per stage and a k-loop unrolled by the stage count:
   // every address is then a compile-time stage base plus a lane offset.
   __shared__ __align__(16) char stage0[DM_STAGE];
@@ -640,79 +642,83 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const bool a_role = wave < 2;
-  const int wv = wave & 1;
   const int nkt = (int)((t.R + DM_BK - 1) / DM_BK);
-  // The waves that load the gathered operand (x is A unless TRANS_B).
-  const bool gath = GATH && (a_role == ((GX == 1) != TRANS_B));
-
-  // This wave's operand: buffer resource, per-chunk byte offsets at k-tile 0
-  // and the per-k-tile advance.
-  const char* obase = a_role ? t.a : t.b;
-  const int64_t ld = a_role ? t.lda : t.ldb;
-  const bool kmaj = a_role ? Lay::A_K : Lay::B_K;
-  const int64_t orow0 = a_role ? t.i0 : t.j0;
-  int64_t obytes;
-  if (a_role) obytes = (Lay::A_K ? t.nrows : t.R) * t.lda * 2;
-  else obytes = (MODE == MODE_WGRAD) ? t.R * t.ldb * 2 : K * N * 2;
-  if (gath) {  // the whole source
-    obase = GX == 1 ? p0 : p1;
-    obytes = gsrc_rows * ld * 2;
-  }
-  const i32x4 rsrc = make_rsrc(obase, obytes);
+  // Operand tiles are loaded in 16 units each (K-major: 16 rows; MN-major: a
+  // pair of k-rows), one 1 KiB chunk per unit. Packed operands: waves 0-1
+  // load A and waves 2-3 B, eight units each (chunk q: unit 8 (wave % 2) + q).
+  // With a gathered operand every wave loads a quarter of each tile instead
+  // (chunks q = 0..3: units 4 wave + q of A, q = 4..7: the same units of B),
+  // so the gathered operand's offset work falls on all four waves alike: with
+  // A on two waves and B on the other two, the two loading the gathered
+  // operand were about 250 cycles per k-tile slower and the others waited for
+  // them (gathered Qwen weight gradients 2-3 % faster this way); packed
+  // operands keep one operand per wave (2 % faster on Qwen's fc1).
+  // GO: the gathered operand (0 A, 1 B; x is A unless TRANS_B).
+  constexpr int GO = ((GX == 1) != TRANS_B) ? 0 : 1;
+  auto chunk_op = [&](int q) { return GATH ? (q >> 2) : (wave < 2 ? 0 : 1); };
+  auto chunk_unit = [&](int q) { return GATH ? 4 * wave + (q & 3) : 8 * (wave & 1) + q; };
+  const int64_t ldo[2] = {t.lda, t.ldb};
+  const int64_t orow[2] = {t.i0, t.j0};
+  const int64_t abytes = (Lay::A_K ? t.nrows : t.R) * t.lda * 2;
+  const int64_t bbytes = (MODE == MODE_WGRAD) ? t.R * t.ldb * 2 : K * N * 2;
+  // Per operand: its buffer resource (the whole source for the gathered one)
+  // and the per-k-tile advance; per chunk: the byte offset at k-tile 0.
+  i32x4 rs[2];
+  rs[0] = (GATH && GO == 0) ? make_rsrc(GX == 1 ? p0 : p1, gsrc_rows * t.lda * 2)
+                            : make_rsrc(t.a, abytes);
+  rs[1] = (GATH && GO == 1) ? make_rsrc(GX == 1 ? p0 : p1, gsrc_rows * t.ldb * 2)
+                            : make_rsrc(t.b, bbytes);
+  uint32_t kst[2];
+  kst[0] = Lay::A_K ? (uint32_t)(DM_BK * 2) : (uint32_t)(DM_BK * t.lda * 2);
+  kst[1] = Lay::B_K ? (uint32_t)(DM_BK * 2) : (uint32_t)(DM_BK * t.ldb * 2);
   uint32_t voff[8];
   int kof[8];
-  uint32_t kstep;
-  if (kmaj) {
-    const int c = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t r = orow0 + 128 * wv + 16 * q + (lane >> 2);
+  for (int q = 0; q < 8; ++q) {
+    const int op = chunk_op(q), u = chunk_unit(q);
+    const int64_t ld = ldo[op];
+    if (op == 0 ? Lay::A_K : Lay::B_K) {
+      const int c = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3
+      const int64_t r = orow[op] + 16 * u + (lane >> 2);
       voff[q] = (uint32_t)((r * ld + 8 * c) * 2);
       kof[q] = 8 * c;
-    }
-    kstep = DM_BK * 2;
-  } else {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int kr = 2 * (wv * 8 + q) + (lane >> 5);
+    } else {
+      const int kr = 2 * u + (lane >> 5);
       const int c = (lane & 31) ^ (4 * (kr & 3));
-      voff[q] = (uint32_t)((kr * ld + orow0 + 8 * c) * 2);
+      voff[q] = (uint32_t)((kr * ld + orow[op] + 8 * c) * 2);
       kof[q] = kr;
     }
-    kstep = (uint32_t)(DM_BK * ld * 2);
   }
-  const uint32_t dst_wave = (a_role ? 0u : (uint32_t)DM_TILE) + (uint32_t)wv * 8192u;
   const int kvalid = (int)t.R;
 
   // Gathered operand: the k-tile's source rows come through the LDS index
-  // ring (a group of four k-tiles per dword DMA, issued five k-tiles ahead of
-  // its first use so the pipeline's waits cover it). A step reads the rows of
-  // the k-tile it will load at the end of its first half, so the LDS reads
+  // ring (a group of eight k-tiles per dword DMA, issued five k-tiles ahead
+  // of its first use so the pipeline's waits cover it). A step reads the rows
+  // of the k-tile it will load at the end of its first half, so the LDS reads
   // are in flight across the wait and barrier, and turns them into offsets
   // after the barrier (reading them where the loads go out, or just before
   // them, was 4-16 % slower): each chunk's offset is its source row's plus
   // the lane's column chunk (two, by k-row parity). Reduction rows past the
   // expert's end read as zeros.
   // gof: the chunks' offsets; fixed (the k-tile's advance is in the resource)
-  // except for the gathered operand's waves, which set them per k-tile.
-  uint32_t grow_v[8], gof[8], gcol[2];
+  // except for the gathered operand's chunks, set per k-tile.
+  uint32_t grow_v[4], gof[8], gcol[2];
 #pragma unroll
   for (int q = 0; q < 8; ++q) gof[q] = voff[q];
-  const uint32_t ld2 = (uint32_t)(ld * 2);
+  const uint32_t ld2 = (uint32_t)(ldo[GO] * 2);
   const i32x4 irsrc = make_rsrc(grow, GATH ? M * 4 : 0);
   if constexpr (GATH) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int c = (lane & 31) ^ (4 * ((2 * p + (lane >> 5)) & 3));
-      gcol[p] = (uint32_t)((orow0 + 8 * c) * 2);
+      gcol[p] = (uint32_t)((orow[GO] + 8 * c) * 2);
     }
   }
   auto issue_idx = [&](int grp) {
-    const int j = lane >> 4, h = (lane >> 3) & 1, q = lane & 7;
-    const int64_t row = (int64_t)(4 * grp + j) * DM_BK + 2 * (wv * 8 + q) + h;
+    const int j = lane >> 3, h = (lane >> 2) & 1, q = lane & 3;
+    const int64_t row = (int64_t)(8 * grp + j) * DM_BK + 8 * wave + 2 * q + h;
     dma4((uint32_t)((t.seg0 + row) * 4), irsrc,
-         lds_addr_of((lds_char*)gidx) + (uint32_t)((wv * 2 + (grp & 1)) * 256));
+         lds_addr_of((lds_char*)gidx) + (uint32_t)((wave * 2 + (grp & 1)) * 256));
   };
   const uint32_t gsrc = (uint32_t)gsrc_rows;
   // An entry outside [0, gsrc_rows) (a negative one reads as a large
@@ -721,47 +727,53 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   // (gsrc_rows + 1) * ld * 2 below 4 GiB, so the offset does not wrap, and
   // gsrc_rows and ld * 2 below 2^24, so the product takes the 24-bit
   // multiply-add). Only an expert's last k-tile has rows past its end.
-  auto offsets = [&](int kk) {  // byte offsets of k-tile kk's chunks from its rows
+  auto offsets = [&](int kk) {  // byte offsets of k-tile kk's gathered chunks from their rows
     if ((kk + 1) * DM_BK <= kvalid) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
-        gof[q] = (uint32_t)__umul24(min(grow_v[q], gsrc), ld2) + gcol[q & 1];
+      for (int q = 0; q < 4; ++q)
+        gof[4 * GO + q] = (uint32_t)__umul24(min(grow_v[q], gsrc), ld2) + gcol[q & 1];
     } else {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int row = kk * DM_BK + 2 * (wv * 8 + q) + (lane >> 5);
-        gof[q] = row < kvalid ? (uint32_t)__umul24(min(grow_v[q], gsrc), ld2) + gcol[q & 1]
+      for (int q = 0; q < 4; ++q) {
+        const int row = kk * DM_BK + 8 * wave + 2 * q + (lane >> 5);
+        gof[4 * GO + q] = row < kvalid
+                              ? (uint32_t)__umul24(min(grow_v[q], gsrc), ld2) + gcol[q & 1]
                               : DM_OOB;
       }
     }
   };
-  auto read_rows = [&](int kk) {  // source rows of k-tile kk's eight chunks
-    lds_char* const ring = (lds_char*)gidx + (wv * 2 + ((kk >> 2) & 1)) * 256;
-    const uint32_t at = (uint32_t)(((kk & 3) * 16 + (lane >> 5) * 8) * 4);
-    const uint4 i0 = read_k(ring, at), i1 = read_k(ring, at + 16);
+  auto read_rows = [&](int kk) {  // source rows of k-tile kk's four gathered chunks
+    lds_char* const ring = (lds_char*)gidx + (wave * 2 + ((kk >> 3) & 1)) * 256;
+    const uint32_t at = (uint32_t)(((kk & 7) * 8 + (lane >> 5) * 4) * 4);
+    const uint4 i0 = read_k(ring, at);
     grow_v[0] = i0.x; grow_v[1] = i0.y; grow_v[2] = i0.z; grow_v[3] = i0.w;
-    grow_v[4] = i1.x; grow_v[5] = i1.y; grow_v[6] = i1.z; grow_v[7] = i1.w;
   };
 
-  // The resource of k-tile kt's loads: advanced by kt k-tiles (the chunk
-  // offsets stay fixed, so a load needs no vector arithmetic), or the whole
-  // source for the gathered operand (its offsets are absolute).
-  auto tile_rsrc = [&](int kt) -> i32x4 {
-    if constexpr (GATH) {
-      if (gath) return rsrc;
-    }
-    return advance_rsrc(rsrc, (uint32_t)kt * kstep);
+  // The resources of k-tile kt's loads: each advanced by kt k-tiles (the
+  // chunk offsets stay fixed, so a load needs no vector arithmetic), except
+  // the gathered operand's (the whole source: its offsets are absolute).
+  struct Rs2 {
+    i32x4 r[2];
+  };
+  auto tile_rsrc = [&](int kt) -> Rs2 {
+    Rs2 o;
+    o.r[0] = (GATH && GO == 0) ? rs[0] : advance_rsrc(rs[0], (uint32_t)kt * kst[0]);
+    o.r[1] = (GATH && GO == 1) ? rs[1] : advance_rsrc(rs[1], (uint32_t)kt * kst[1]);
+    return o;
   };
   // Chunk q of k-tile kt into stage `stg` through rr = tile_rsrc(kt).
-  auto issue_one = [&](lds_char* stg, const i32x4& rr, int kt, int q) {
+  auto issue_one = [&](lds_char* stg, const Rs2& rr, int kt, int q) {
+    const int op = chunk_op(q);
     uint32_t off = gof[q];
     if constexpr (KMASK) {
-      if (kmaj && kt * DM_BK + kof[q] >= kvalid) off = DM_OOB;
+      if ((op == 0 ? Lay::A_K : Lay::B_K) && kt * DM_BK + kof[q] >= kvalid) off = DM_OOB;
     }
-    dma16(off, rr, lds_addr_of(stg) + dst_wave + (uint32_t)q * 1024u);
+    dma16(off, op == 0 ? rr.r[0] : rr.r[1],
+          lds_addr_of(stg) + (op == 0 ? 0u : (uint32_t)DM_TILE) +
+              (uint32_t)chunk_unit(q) * 1024u);
   };
   auto issue = [&](lds_char* stg, int kt) {
-    const i32x4 rr = tile_rsrc(kt);
+    const Rs2 rr = tile_rsrc(kt);
 #pragma unroll
     for (int q = 0; q < 8; ++q) issue_one(stg, rr, kt, q);
   };
@@ -828,22 +840,21 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
       mfma(i, a0, b0, decltype(first_c)::value);
       if (i < FM + FN) frag(cur, 1, i, a1, b1);
       if constexpr (GATH) {
-        if (i == FM * FN - 1 && gath) read_rows(kt + 3);  // in flight across the wait
+        if (i == FM * FN - 1) read_rows(kt + 3);  // in flight across the wait
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     TT_WAIT_VMCNT(8);
     __builtin_amdgcn_s_barrier();
     if constexpr (GATH) {
-      // Indices of k-tiles kt + 5 .. kt + 8 go out before this step's loads,
-      // so the next step's wait covers them before step kt + 2 reads them.
-      if (gath) {
-        if ((kt & 3) == 3) issue_idx((kt + 5) >> 2);
-        offsets(kt + 3);
-      }
+      // Indices of k-tiles kt + 5 .. kt + 12 go out before this step's loads,
+      // so the next step's wait covers them before step kt + 2 reads them
+      // (groups 0 and 1 went out before the prologue).
+      if ((kt & 7) == 3 && kt > 3) issue_idx((kt + 5) >> 3);
+      offsets(kt + 3);
     }
     refresh();
-    const i32x4 rr = tile_rsrc(kt + 3);
+    const Rs2 rr = tile_rsrc(kt + 3);
 #pragma unroll
     for (int i = 0; i < FM * FN; ++i) {
       mfma(i, a1, b1);
@@ -854,18 +865,14 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
   };
 
   if constexpr (GATH) {
-    if (gath) {
-      issue_idx(0);
-      issue_idx(1);
-      TT_WAIT_VMCNT(0);
-    }
+    issue_idx(0);
+    issue_idx(1);
+    TT_WAIT_VMCNT(0);
   }
   auto issue_first = [&](lds_char* stg, int kk) {
     if constexpr (GATH) {
-      if (gath) {
-        read_rows(kk);
-        offsets(kk);
-      }
+      read_rows(kk);
+      offsets(kk);
     }
     issue(stg, kk);
   };
