@@ -792,19 +792,21 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
 
   f32x16 acc[FM][FN];  // set by the first k-step (a zero accumulator operand)
 
-  // Current fragment offsets, re-materialised once per half step so that the
-  // compiler keeps one register per offset instead of one per stage.
+  // Current fragment offsets, made opaque once per half step (an empty asm on
+  // the originals, no copies) so that the compiler keeps one register per
+  // offset instead of one per stage. Copying them into fresh registers
+  // instead cost 8 moves per half step: 1-2 % of the weight gradients.
   uint32_t ao[2], bo[2], am[FM], bm[FN];
   auto refresh = [&]() {
+    if constexpr (Lay::A_K) asm volatile("" : "+v"(a_off[0]), "+v"(a_off[1]));
+    else asm volatile("" : "+v"(a_mn[0]), "+v"(a_mn[1]), "+v"(a_mn[2]), "+v"(a_mn[3]));
+    if constexpr (Lay::B_K) asm volatile("" : "+v"(b_off[0]), "+v"(b_off[1]));
+    else asm volatile("" : "+v"(b_mn[0]), "+v"(b_mn[1]), "+v"(b_mn[2]), "+v"(b_mn[3]));
     ao[0] = a_off[0]; ao[1] = a_off[1]; bo[0] = b_off[0]; bo[1] = b_off[1];
 #pragma unroll
     for (int i = 0; i < FM; ++i) am[i] = a_mn[i];
 #pragma unroll
     for (int i = 0; i < FN; ++i) bm[i] = b_mn[i];
-    if constexpr (Lay::A_K) asm volatile("" : "+v"(ao[0]), "+v"(ao[1]));
-    else asm volatile("" : "+v"(am[0]), "+v"(am[1]), "+v"(am[2]), "+v"(am[3]));
-    if constexpr (Lay::B_K) asm volatile("" : "+v"(bo[0]), "+v"(bo[1]));
-    else asm volatile("" : "+v"(bm[0]), "+v"(bm[1]), "+v"(bm[2]), "+v"(bm[3]));
   };
   // Fragment unit i (0..FM-1: A block i, FM..: B block i - FM) of k-step s.
   auto frag = [&](lds_char* stg, int s, int i, uint4 (&fa)[FM], uint4 (&fb)[FN]) {
@@ -846,6 +848,9 @@ __global__ __launch_bounds__(DM_NT) void gmm_mfma_kernel(const char* __restrict_
     }
     TT_WAIT_VMCNT(8);
     __builtin_amdgcn_s_barrier();
+    // Nothing moves above the barrier: the gathered rows' clamps would wait
+    // there for the ring reads that are meant to be in flight across it.
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (GATH) {
       // Indices of k-tiles kt + 5 .. kt + 12 go out before this step's loads,
       // so the next step's wait covers them before step kt + 2 reads them
@@ -1402,17 +1407,19 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   for (int ni = 0; ni < FN; ++ni) b_mn[ni] = fragmn_base(wn * WT + ni * 32, lane) + P_OPND;
 
   uint32_t ao, bo, am[FM], bm[FN];
-  // Offsets for k-step s, re-materialised per use (one register each).
+  // Offsets for k-step s, made opaque per use (an empty asm on the originals,
+  // no copies: one register each). Copies into fresh registers cost about 20
+  // moves per k-tile: 1-3 % of the forward GEMMs.
   auto refresh = [&](int s) {
+    if constexpr (Lay::A_K) asm volatile("" : "+v"(a_k[s]));
+    else asm volatile("" : "+v"(a_mn[0]), "+v"(a_mn[1]), "+v"(a_mn[2]), "+v"(a_mn[3]));
+    if constexpr (Lay::B_K) asm volatile("" : "+v"(b_k[s]));
+    else asm volatile("" : "+v"(b_mn[0]), "+v"(b_mn[1]), "+v"(b_mn[2]), "+v"(b_mn[3]));
     ao = a_k[s]; bo = b_k[s];
 #pragma unroll
     for (int i = 0; i < FM; ++i) am[i] = a_mn[i];
 #pragma unroll
     for (int i = 0; i < FN; ++i) bm[i] = b_mn[i];
-    if constexpr (Lay::A_K) asm volatile("" : "+v"(ao));
-    else asm volatile("" : "+v"(am[0]), "+v"(am[1]), "+v"(am[2]), "+v"(am[3]));
-    if constexpr (Lay::B_K) asm volatile("" : "+v"(bo));
-    else asm volatile("" : "+v"(bm[0]), "+v"(bm[1]), "+v"(bm[2]), "+v"(bm[3]));
   };
   // Fragment i of k-step s for a tile whose waves multiply MV of their four
   // 32-row blocks: A blocks 0 .. MV - 1, then the four B blocks.
