@@ -228,27 +228,28 @@ struct WgradRank {
 constexpr int WR_MAX_E = 4096;
 __device__ WgradRank g_wgrad_rank[WQ_SLOTS * WR_MAX_E];
 
-// One thread per expert (grid ceil(E / 256)); each block scans all the counts
-// and ranks its experts against all of them. Counts sum to at most M < 2^31
-// rows (the launchers' 32-bit offset limits), so they compare as int.
+// One thread per expert (grid ceil(E / 256)); every block reads all the
+// counts into LDS and each thread makes one pass over them: its rank (the
+// experts ahead of it) and its first row (the rows of the experts before it).
+// Counts sum to at most M < 2^31 rows (the launchers' 32-bit offset limits),
+// so they compare as int; the first row is summed in 64 bits.
 __global__ __launch_bounds__(256) void wgrad_rank_kernel(const int64_t* __restrict__ counts, int E,
                                                          int slot) {
-  __shared__ int64_t row_start[WR_MAX_E + 1];
-  __shared__ int tile_start[WR_MAX_E + 1];
   __shared__ int cnt[WR_MAX_E];
-  scan_counts<256>(counts, E, 1, row_start, tile_start);
-  for (int x = threadIdx.x; x < E; x += 256) cnt[x] = (int)(row_start[x + 1] - row_start[x]);
+  for (int y = threadIdx.x; y < E; y += 256) cnt[y] = (int)counts[y];
   __syncthreads();
   const int x = blockIdx.x * 256 + threadIdx.x;
   if (x >= E) return;
   const int cx = cnt[x];
   int r = 0;
+  int64_t start = 0;
 #pragma unroll 8
   for (int y = 0; y < E; ++y) {
     const int cy = cnt[y];
     r += (cy > cx) | ((cy == cx) & (y < x));
+    start += y < x ? cy : 0;
   }
-  g_wgrad_rank[slot * WR_MAX_E + r] = WgradRank{row_start[x], cx, x};
+  g_wgrad_rank[slot * WR_MAX_E + r] = WgradRank{start, cx, x};
 }
 
 // PAIRS: weight-gradient tiles on XCD pairs (wgrad_pair_split); the launch
