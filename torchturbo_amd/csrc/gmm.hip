@@ -20,10 +20,15 @@
 //   MN-major tiles keep their natural [k][row] order and are read with the
 //   gfx950 transposing load ds_read_b64_tr_b16 (no register transpose).
 //   MFMAs, fragment reads of the next k-step and DMA issue are interleaved
-//   one per slot. The epilogue converts to 16 bits in hardware and stores
+//   one per slot; a chunk's offset is fixed and the k-tile's advance lives in
+//   the buffer resource (scalar registers), so a load needs no vector
+//   instruction. With rows gathered through a row map, every wave loads a
+//   quarter of both operand tiles and turns its rows into offsets after the
+//   k-tile barrier. The epilogue converts to 16 bits in hardware and stores
 //   through LDS as full 256-byte rows. Serves wgrad with long expert
-//   reductions (its three k-tiles in flight stream two activation operands
-//   fastest) and short fwd/dgrad reductions.
+//   reductions over fewer than 512 output tiles per expert (its three
+//   k-tiles in flight stream two activation operands fastest), the gathering
+//   weight gradients, and short fwd/dgrad reductions.
 // * gmm_p64_kernel (bf16/f16 fwd/dgrad with a reduction longer than 64, and
 //   wgrad with few rows per expert): persistent, one block per CU; fwd/dgrad
 //   blocks walk a strided list of output tiles, wgrad blocks take tickets
@@ -62,8 +67,9 @@
 // exit. fwd/dgrad block ids are remapped so that consecutive slots (sharing an
 // A panel and an expert's weights) run on one XCD and its L2. wgrad blocks
 // take experts longest-first; each expert's tiles go to one pair of XCDs
-// (one-tile-per-block kernel) or to every XCD as rectangles (persistent
-// kernel), so that the XCDs share its activation panels in L2.
+// (one-tile-per-block kernel, whose blocks read the launch's ranking from
+// wgrad_rank_kernel) or to every XCD as rectangles (persistent kernel), so
+// that the XCDs share its activation panels in L2.
 #include "common.h"
 
 #include <atomic>
