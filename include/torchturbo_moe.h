@@ -251,7 +251,9 @@ int tt_gated_act_bwd(const void* x, int dtype, int64_t rows, int64_t ffn, int ac
  * least 512 output tiles of 256x256 per expert; tt_gmm_wgrad_persistent), or
  * the one-tile-per-block kernel's expert ranking. At most 64 weight-gradient
  * launches may be in flight at once across all streams of a device; launches
- * on one stream never overlap, so a single stream has no limit.
+ * on one stream never overlap, so a single stream has no limit. A launch
+ * captured into a graph keeps its slot in every replay, so replays of one
+ * graph must not overlap each other.
  * fwd:   y[M, N] = x[M, K] @ W[e] with W [E, K, N]; trans_b: W [E, N, K], W[e]^T. */
 int tt_gmm_fwd(const void* x, const void* w, int dtype, int64_t m, int64_t k, int64_t n,
                int32_t num_experts, int32_t trans_b, const int64_t* counts, void* y,
