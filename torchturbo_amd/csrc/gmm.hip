@@ -2151,6 +2151,16 @@ __global__ __launch_bounds__(DM_NT) void gmm_q8_kernel(const char* __restrict__ 
   // B: per chunk (fwd, 16 rows) or per four chunks (dgrad, 8 k-rows).
   const uint32_t b_qstep = MODE == MODE_FWD ? (uint32_t)(16 * K) : (uint32_t)(8 * K);
   const uint32_t b_kstep = MODE == MODE_FWD ? (uint32_t)Q_BK : (uint32_t)(Q_BK * K);
+  // Each chunk's offset from the tile origin, fixed for the launch: a load
+  // needs no vector arithmetic; the k-tile moves the buffer resource instead
+  // (scalar arithmetic, range checks unchanged).
+  uint32_t a_chunk[4], b_chunk[8];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) a_chunk[q] = ((q & 1) ? a_odd : a_even) + (uint32_t)(q >> 1) * a_qstep;
+#pragma unroll
+  for (int qb = 0; qb < 8; ++qb)
+    b_chunk[qb] = (MODE == MODE_FWD ? b_base[0] : b_base[qb & 3]) +
+                  (uint32_t)(MODE == MODE_FWD ? qb : qb >> 2) * b_qstep;
 
   auto rsrc_a = [&](const TileDesc& t, bool valid) -> i32x4 {
     if (!valid) return make_rsrc(p0, 0);
@@ -2205,23 +2215,19 @@ __global__ __launch_bounds__(DM_NT) void gmm_q8_kernel(const char* __restrict__ 
     uint32_t off, dst;
     i32x4 rs;
     if (q < 4) {
-      uint32_t vb = (q & 1) ? a_odd : a_even;
-      asm volatile("" : "+v"(vb));
-      off = vb + ((uint32_t)(q >> 1) * a_qstep + (uint32_t)k * (Q_BK * 2));
+      off = a_chunk[q];
       if constexpr (KMASK) {
         if (k * Q_BK + ((q & 1) ? a_kof_odd : a_kof_even) >= kvalid) off = DM_OOB;
       }
-      rs = nxt ? ra_nxt : ra_cur;
+      rs = advance_rsrc(nxt ? ra_nxt : ra_cur, (uint32_t)k * (Q_BK * 2));
       dst = (uint32_t)(4 * wave + q) * 1024u;
     } else {
       const int qb = q - 4;
-      uint32_t vb = MODE == MODE_FWD ? b_base[0] : b_base[qb & 3];
-      asm volatile("" : "+v"(vb));
-      off = vb + ((uint32_t)(MODE == MODE_FWD ? qb : qb >> 2) * b_qstep + (uint32_t)k * b_kstep);
+      off = b_chunk[qb];
       if constexpr (KMASK && MODE == MODE_FWD) {
         if (k * Q_BK + b_kof >= kvalid) off = DM_OOB;
       }
-      rs = nxt ? rb_nxt : rb_cur;
+      rs = advance_rsrc(nxt ? rb_nxt : rb_cur, (uint32_t)k * b_kstep);
       dst = (uint32_t)Q_A + (uint32_t)(8 * wave + qb) * 1024u;
     }
     dma16(off, rs, lds_addr_of(stg) + dst);
@@ -2263,12 +2269,24 @@ __global__ __launch_bounds__(DM_NT) void gmm_q8_kernel(const char* __restrict__ 
 
   f32x16 acc[FM][FN];
   uint32_t ao, bo[FN];
-  auto refresh = [&](int s) {
-    ao = a_k[s];
-    asm volatile("" : "+v"(ao));
+  uint32_t b_d[FN];  // dgrad: B fragment offsets of k-step 0
 #pragma unroll
-    for (int i = 0; i < FN; ++i) bo[i] = b_off(s, i);
-    asm volatile("" : "+v"(bo[0]), "+v"(bo[1]), "+v"(bo[2]), "+v"(bo[3]));
+  for (int i = 0; i < FN; ++i) b_d[i] = MODE == MODE_FWD ? 0u : b_off(0, i);
+  auto refresh = [&](int s) {
+    asm volatile("" : "+v"(a_k[s]));
+    ao = a_k[s];
+    if constexpr (MODE == MODE_FWD) {
+      // One opaque register per k-step; the column blocks are immediate offsets.
+      asm volatile("" : "+v"(b_f[s]));
+#pragma unroll
+      for (int i = 0; i < FN; ++i) bo[i] = b_off(s, i);
+    } else {
+      // b_off(s, ni) = b_off(0, ni) + 8192 s: four opaque registers for the
+      // column blocks, the k-step an immediate offset.
+      asm volatile("" : "+v"(b_d[0]), "+v"(b_d[1]), "+v"(b_d[2]), "+v"(b_d[3]));
+#pragma unroll
+      for (int i = 0; i < FN; ++i) bo[i] = b_d[i] + (uint32_t)s * 8192u;
+    }
   };
   auto read_b8 = [&](lds_char* stg, uint32_t off) -> uint2 {
     if constexpr (MODE == MODE_FWD) {
