@@ -1295,6 +1295,16 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     }
   }
 
+  // Each chunk's offset from the tile origin, fixed for the launch; the
+  // k-tile moves the buffer resource (scalar arithmetic) instead.
+  uint32_t choff[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int op = q < 8 ? 0 : 1, qq = q & 7;
+    choff[q] = ((qq & 1) ? vodd[op] : vbase[op]) + (uint32_t)(qq >> 1) * qstep[op];
+  }
+  const uint32_t ks_a = (uint32_t)__builtin_amdgcn_readfirstlane((int)kstep[0]);
+  const uint32_t ks_b = (uint32_t)__builtin_amdgcn_readfirstlane((int)kstep[1]);
   // Resources based at the tile origin. fwd / dgrad: A is K-major (the
   // expert's rows), B the expert's weights. wgrad: both operands are
   // MN-major over the expert's rows, so reduction rows past the expert's
@@ -1354,10 +1364,12 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
       ro[q] = row < t.nrows && v < (uint32_t)asrc_rows ? v : GA_NOROW;
     }
   };
+  // Byte offsets of the lane's A chunks in the source (row and k-chunk).
   auto gather_offsets = [&](uint32_t (&ro)[8]) {
 #pragma unroll
     for (int q = 0; q < 8; ++q)
-      ro[q] = ro[q] == GA_NOROW ? GA_NOROW : ro[q] * (uint32_t)(lda * 2);
+      ro[q] = ro[q] == GA_NOROW ? GA_NOROW
+                                : ro[q] * (uint32_t)(lda * 2) + (uint32_t)(2 * ((q & 1) ? kof_odd : kof));
   };
   if constexpr (GA) {
     gather_rows(tc, true, ro_cur);
@@ -1377,19 +1389,15 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     const int op = is_a ? 0 : 1;
     const bool kmaj = is_a ? Lay::A_K : Lay::B_K;
     const int qq = q & 7;
-    uint32_t vb = (qq & 1) ? vodd[op] : vbase[op];
-    asm volatile("" : "+v"(vb));  // one register per base, not one per chunk
-    uint32_t off = vb + ((uint32_t)(qq >> 1) * qstep[op] + (uint32_t)k * kstep[op]);
+    uint32_t off = choff[q];
     if constexpr (GA) {
-      // The row's source offset plus the lane's chunk and the k-tile.
-      if (is_a)
-        off = (nxt ? ro_nxt[qq] : ro_cur[qq]) + (uint32_t)(2 * ((qq & 1) ? kof_odd : kof)) +
-              (uint32_t)k * kstep[op];
+      if (is_a) off = nxt ? ro_nxt[qq] : ro_cur[qq];  // the row's source offset and k-chunk
     }
     if constexpr (KMASK) {
       if (kmaj && k * P_BK + ((qq & 1) ? kof_odd : kof) >= kvalid) off = DM_OOB;
     }
-    const i32x4 rs = is_a ? (nxt ? ra_nxt : ra_cur) : (nxt ? rb_nxt : rb_cur);
+    const i32x4 rs = advance_rsrc(is_a ? (nxt ? ra_nxt : ra_cur) : (nxt ? rb_nxt : rb_cur),
+                                  (uint32_t)k * (is_a ? ks_a : ks_b));
     dma16(off, rs, lds_addr_of(stg) + (is_a ? 0u : (uint32_t)P_OPND) +
                        (uint32_t)(8 * wave + (q & 7)) * 1024u);
   };
