@@ -35,7 +35,8 @@
 //   from per-XCD queues over the experts' tiles, longest expert first, and
 //   claim the next ticket two or three k-tiles before the current tile ends.
 //   256x256x64 tiles through two 64 KiB LDS stages, so K-major rows are
-//   whole 128-byte lines. The k-tiles of consecutive tiles form one stream
+//   whole 128-byte lines. Loads as in gmm_mfma_kernel: fixed chunk offsets,
+//   the k-tile in the buffer resource. The k-tiles of consecutive tiles form one stream
 //   (the next tile's first loads overlap the current tile's last k-tile and
 //   epilogue); the epilogue stages through a private 4 KiB of LDS per wave
 //   and stores with buffer stores whose resource ends at the expert's last
@@ -51,7 +52,9 @@
 //   its own fragments as e4m3 bytes (plain 8-byte reads of K-major rows in
 //   fwd, the transposing 8-bit read ds_read_b64_tr_b8 of N-major rows in
 //   dgrad) and dequantises them in registers between its MFMAs, exactly
-//   bf16(f32(q) * f32(scale)) with one scale per wave and k-tile.
+//   bf16(f32(q) * f32(scale)) with one scale per wave and k-tile. Loads use
+//   fixed chunk offsets with the k-tile in the buffer resource, so the
+//   k-loop's vector instructions are almost all the dequantisation.
 // * gmm_fp8_kernel (FP8 fwd/dgrad with a reduction of one k-tile): the
 //   256x256x32 tiles of gmm_mfma_kernel; the weight tile arrives in LDS as
 //   e4m3 bytes and each wave decodes its own rows in hardware, multiplies by
