@@ -175,7 +175,31 @@ def gpu_run(w, steps, warmup):
     t1 = time.perf_counter()
     L.set_timer(None)
     kernels = timer.elapsed_ms()
-    return (t1 - t0) * 1e3 / steps, kernels
+    order = [(n, a.elapsed_time(b)) for n, a, b in timer.events if n in GEMM_ENTRIES]
+    return (t1 - t0) * 1e3 / steps, kernels, order
+
+
+GEMM_KINDS = ("fc1_fwd", "fc2_fwd", "fc2_dgrad", "fc2_wgrad", "fc1_dgrad", "fc1_wgrad")
+
+
+def per_gemm(w, order, steps):
+    """Mean HIP-event time and TFLOP/s of each of the step's six grouped GEMMs,
+    told apart by launch order (forward fc1, fc2; backward fc2 dgrad, fc2
+    wgrad, fc1 dgrad, fc1 wgrad). None when the launches do not follow it."""
+    if steps < 1 or len(order) != 6 * steps:
+        return None
+    for i, kind in enumerate(GEMM_KINDS):
+        names = {n for n, _ in order[i::6]}
+        op = kind.split("_")[1]
+        if len(names) != 1 or op not in next(iter(names)):
+            return None
+    M, H, F = w.routed_rows, w.hidden, w.ffn
+    out = {}
+    for i, kind in enumerate(GEMM_KINDS):
+        us = sum(t for _, t in order[i::6]) / steps * 1e3
+        flops = 2.0 * M * H * 2 * F if kind.startswith("fc1") else 2.0 * M * F * H
+        out[kind] = {"entry": order[i][0], "us": round(us, 1), "tflops": round(flops / us / 1e6, 1)}
+    return out
 
 
 def router_run(w, steps, warmup):
@@ -391,7 +415,7 @@ def main():
     if args.part == "dense-compare":
         print(json.dumps(dense_compare(w, max(args.steps, 1))), flush=True)
         return
-    ms, kernels = gpu_run(w, args.steps, args.warmup)
+    ms, kernels, order = gpu_run(w, args.steps, args.warmup)
     tokens_per_s = w.tokens / (ms / 1e3)
 
     gemm_launches = sum(kernels.get(n, (0, 0.0))[0] for n in GEMM_ENTRIES)
@@ -448,6 +472,7 @@ def main():
             "launches": gemm_launches,
             "avg_launch_us": round(avg_launch_s * 1e6, 1),
             "gemm_ms_per_step": round(gemm_ms / args.steps, 3),
+            "per_gemm": per_gemm(w, order, args.steps),
         },
         "permute": {
             "bound": "hbm", "unit": "GB/s", "peak": HBM_PEAK_GBS,
