@@ -1199,6 +1199,91 @@ __device__ __forceinline__ int wgrad_tile_at(int q, int cls, int nx, int cx, con
   return nkt > 2 ? nkt : 2;
 }
 
+// Cost-sorted schedule for fwd / dgrad launches of at most LPT_MAX_TJ n-tiles per
+// m-tile, whose slots differ most in cost (a slot of two thin tiles costs
+// about 1.2 full tiles, a single thin tile 0.6). The static schedule hands
+// every XCD its consecutive positions round by round; here each round's slots
+// of an XCD, heaviest first, go to that XCD's blocks least loaded so far, so
+// the same slots still run on the same XCD in the same round (shared operand
+// panels in its L2). Qwen3-30B-A3B's gathered fc2 data gradient (three n-tiles,
+// seven rounds): 424 -> 407 us with the assignment computed here (410 -> 379 us
+// with a table computed on the host). Launches with six or more n-tiles gained
+// 0-1 % from the host table and keep the static order; so do launches of many
+// rounds, where the assignment costs more (one round of slot decoding and
+// ranking each) and the last partial round weighs less: the varlen stress
+// layer's fc2 data gradient (27 rounds) took 1589 against 1543 us.
+constexpr int LPT_MAX_TJ = 4;
+constexpr int LPT_MAX_ROUNDS = 12;
+
+// Cost of schedule slot s in twentieths of a full tile: 20 full, 17 a partial
+// m-tile of more than 128 rows, 13 of at most 128 rows, 12 per thin tile.
+__device__ int lpt_cost(int s, int E, int tiles_j, const int64_t* row_start,
+                        const int* tile_start) {
+  int lo = 0, hi = E - 1;  // last e with tile_start[e] <= s
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tile_start[mid] <= s) lo = mid; else hi = mid - 1;
+  }
+  const int64_t rows = row_start[lo + 1] - row_start[lo];
+  const int local = s - tile_start[lo];
+  if (rows > 0 && rows <= 64) return 12 * min(2, tiles_j - 2 * local);
+  const int64_t left = rows - (int64_t)(local / tiles_j) * DM_BM;
+  return left >= DM_BM ? 20 : (left <= 128 ? 13 : 17);
+}
+
+// Wave 0 computes the assignment of this block's XCD (lane l = the XCD's
+// block l, positions x Q + l with Q = G / 8) and keeps this block's slots in
+// `slots`; every thread gets the block's slot count. Per round: slots ranked
+// by cost (descending, then position) with one ballot per cost value, blocks
+// ranked by load (ascending, then index); block of load rank i takes the slot
+// of cost rank i. Each slot goes to exactly one block: both ranks are
+// permutations.
+__device__ int lpt_schedule(int total, int G, int E, int tiles_j, const int64_t* row_start,
+                            const int* tile_start, int* slots, int* tmp, int* tmpc,
+                            int* nout) {
+  if (threadIdx.x < 64) {
+    const int l = threadIdx.x;
+    const int Q = G >> 3, base = (int)(blockIdx.x & 7) * Q, me = (int)(blockIdx.x >> 3);
+    const uint64_t below = l == 0 ? 0ull : (~0ull >> (64 - l));
+    const int rounds = (total + G - 1) / G;
+    int acc = 0, mine = 0;
+    for (int k = 0; k < rounds; ++k) {
+      const int s = k * G + base + l;
+      const bool valid = l < Q && s < total;
+      const int c = valid ? lpt_cost(s, E, tiles_j, row_start, tile_start) : 0;
+      const uint64_t m24 = __ballot(valid && c == 24), m20 = __ballot(valid && c == 20);
+      const uint64_t m17 = __ballot(valid && c == 17), m13 = __ballot(valid && c == 13);
+      const uint64_t m12 = __ballot(valid && c == 12);
+      uint64_t heavier = 0, same = m12;
+      if (c == 24) { same = m24; }
+      else if (c == 20) { heavier = m24; same = m20; }
+      else if (c == 17) { heavier = m24 | m20; same = m17; }
+      else if (c == 13) { heavier = m24 | m20 | m17; same = m13; }
+      else { heavier = m24 | m20 | m17 | m13; }
+      const int rc = __popcll(heavier) + __popcll(same & below);
+      const int nvalid = __popcll(m24 | m20 | m17 | m13 | m12);
+      int ra = 0;
+      for (int m = 0; m < Q; ++m) {
+        const int am = __builtin_amdgcn_readlane(acc, m);
+        ra += (am < acc) || (am == acc && m < l);
+      }
+      if (valid) {
+        tmp[rc] = s;
+        tmpc[rc] = c;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (l < Q && ra < nvalid) {
+        acc += tmpc[ra];
+        if (l == me) slots[mine++] = tmp[ra];
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    if (l == me) *nout = mine;
+  }
+  __syncthreads();
+  return *nout;
+}
+
 // GA (fwd / dgrad): the A rows are gathered, row r of the packed order being
 // row arow[r] of p0 ([asrc_rows, lda]); see gather_rows below.
 template <int MODE, bool TRANS_B, int ET, bool KMASK, bool GA = false>
@@ -1232,11 +1317,21 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
   int* ranked = nullptr;
   WgradRect rect{0, 0, 0};
   int q0 = 0;
+  __shared__ int lpt_slots[LPT_MAX_ROUNDS], lpt_tmp[64], lpt_tmpc[64], lpt_n;
+  bool lpt = false;
   if constexpr (!WG) {
     pos = xcd_remap(blockIdx.x, G);
     total = tile_start[E];  // schedule slots
-    if (pos >= total) return;
-    ntiles = (total - pos + G - 1) / G;
+    lpt = tiles_j <= LPT_MAX_TJ && (G & 7) == 0 && G <= 512 &&
+          (total + G - 1) / G <= LPT_MAX_ROUNDS;
+    if (lpt) {
+      ntiles = lpt_schedule(total, G, E, tiles_j, row_start, tile_start, lpt_slots, lpt_tmp,
+                            lpt_tmpc, &lpt_n);
+      if (ntiles == 0) return;
+    } else {
+      if (pos >= total) return;
+      ntiles = (total - pos + G - 1) / G;
+    }
   } else {
     int* cnt = tile_start + E + 1;
     ranked = cnt + 2 * E;
@@ -1254,6 +1349,10 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     q0 = ticket_slot[0];
     if (q0 >= total) return;
   }
+  // Schedule slot of the block's n-th tile (fwd / dgrad).
+  auto slot_of = [&](int n) -> int {
+    return lpt ? __builtin_amdgcn_readfirstlane(lpt_slots[n]) : pos + n * G;
+  };
   const int64_t R = MODE == MODE_FWD ? K : N;  // fwd / dgrad reduction length
   int nkt_c = (int)((R + P_BK - 1) / P_BK);     // >= 2 (host check)
   int nkt_n = nkt_c;
@@ -1338,10 +1437,11 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
                                    ranked, tc);
     has_next = false;  // known at k-tile nkt_c - 2
   } else {
-    tile_at<MODE, TRANS_B, 2>(pos, p0, p1, out, K, N, E, tiles_j, row_start, tile_start, tc);
+    tile_at<MODE, TRANS_B, 2>(slot_of(0), p0, p1, out, K, N, E, tiles_j, row_start, tile_start,
+                              tc);
     has_next = ntiles > 1;
     if (has_next)
-      tile_at<MODE, TRANS_B, 2>(pos + G, p0, p1, out, K, N, E, tiles_j, row_start, tile_start,
+      tile_at<MODE, TRANS_B, 2>(slot_of(1), p0, p1, out, K, N, E, tiles_j, row_start, tile_start,
                                 tn);
   }
   // GA: the source row of each of the lane's eight A rows of a tile (K-major
@@ -1733,7 +1833,7 @@ __global__ __launch_bounds__(DM_NT) void gmm_p64_kernel(const char* __restrict__
     if constexpr (!WG) {
       has_next = n + 2 < ntiles;
       if (has_next)
-        tile_at<MODE, TRANS_B, 2>(pos + (n + 2) * G, p0, p1, out, K, N, E, tiles_j, row_start,
+        tile_at<MODE, TRANS_B, 2>(slot_of(n + 2), p0, p1, out, K, N, E, tiles_j, row_start,
                                   tile_start, tn);
       if constexpr (GA) gather_rows(tn, has_next, ro_nxt);
       ra_nxt = rsrc_a(tn, has_next);
@@ -2600,6 +2700,10 @@ int cu_count() {
 // Dynamic LDS of the persistent kernel: the expert schedule plus the expert
 // ranking of wgrad.
 size_t p64_schedule_bytes(int E) { return schedule_bytes(E) + (size_t)E * sizeof(int); }
+// All LDS of the persistent kernel: stages, epilogue staging, the dynamic
+// schedule and about 1 KiB of small static arrays (tickets, scan partials,
+// the cost-sorted schedule's slot lists).
+size_t p64_lds_bytes(int E) { return p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI + 1024; }
 
 // Weight gradients (ti x tj output tiles per expert) run on the persistent
 // kernel for short reductions (few rows per expert on average, known without
@@ -2616,7 +2720,7 @@ size_t p64_schedule_bytes(int E) { return schedule_bytes(E) + (size_t)E * sizeof
 bool wgrad_persistent(int64_t M, int64_t K, int64_t N, int E, int ti, int tj) {
   const int64_t ld = K > N ? K : N;
   return (M <= (int64_t)E * P_WGRAD_ROWS || (int64_t)ti * tj >= P_WGRAD_TILES) &&
-         p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI <= 160 * 1024 &&
+         p64_lds_bytes(E) <= 160 * 1024 &&
          (M + 2 * P_BK) * ld * 2 < (int64_t)DM_OOB;
 }
 
@@ -2662,7 +2766,7 @@ int launch_mfma(const void* p0, const void* p1, void* out, int64_t M, int64_t K,
              "gmm: operands of 4 GiB or more are not supported (M=%lld K=%lld N=%lld)",
              (long long)M, (long long)K, (long long)N);
   const int64_t R = MODE == MODE_FWD ? K : N;  // reduction length of fwd / dgrad
-  const bool p64_lds = p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI <= 160 * 1024;
+  const bool p64_lds = p64_lds_bytes(E) <= 160 * 1024;
   if constexpr (MODE != MODE_WGRAD) {
     // The persistent kernel needs two k-tiles per output tile, its LDS
     // (stages, epilogue staging, schedule) and 32-bit offsets for loads that
@@ -2695,7 +2799,7 @@ const char* gather_limit(int MODE, int64_t src_rows, int64_t M, int64_t K, int64
   const int64_t J = MODE == MODE_FWD ? N : K;  // output width
   if (!(R > P_BK && R % P_BK == 0))
     return "the reduction length must be a multiple of 64 above 64";
-  if (p64_schedule_bytes(E) + 2 * P_STAGE + 4 * P_EPI > 160 * 1024)
+  if (p64_lds_bytes(E) > 160 * 1024)
     return "too many experts for the LDS tile schedule";
   if (!(src_rows >= 1 && (src_rows * R + 4 * P_BK) * 2 < (int64_t)GA_NOROW))
     return "the source must hold at least one row and less than 2 GiB";
