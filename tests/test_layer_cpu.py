@@ -123,7 +123,7 @@ def test_folded_permutation_shape_rule():
     assert not shapes_pay(16384, 2048, 1536, 8, 128, torch.float32)
     assert not shapes_pay(16384, 2000, 1536, 8, 128, bf)        # hidden not a multiple of 64
     assert not shapes_pay(16384, 64, 128, 8, 16, bf)            # hidden of one k-tile
-    # more experts than the gathering kernels' LDS schedule holds (about 679):
+    # more experts than the gathering kernels' LDS schedule holds (about 636):
     # the layer keeps the permutation instead of failing in forward
     assert shapes_pay(40000, 2048, 1536, 8, 600, bf)
     assert not shapes_pay(131072, 2048, 1536, 8, 1024, bf)
