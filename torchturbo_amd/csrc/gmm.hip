@@ -31,7 +31,9 @@
 //   weight gradients, and short fwd/dgrad reductions.
 // * gmm_p64_kernel (bf16/f16 fwd/dgrad with a reduction longer than 64, and
 //   wgrad with few rows per expert): persistent, one block per CU; fwd/dgrad
-//   blocks walk a strided list of output tiles, wgrad blocks take tickets
+//   blocks walk a strided list of output tiles (launches of at most four
+//   n-tiles and twelve rounds: a cost-sorted list within each XCD, computed
+//   at start by lpt_schedule), wgrad blocks take tickets
 //   from per-XCD queues over the experts' tiles, longest expert first, and
 //   claim the next ticket two or three k-tiles before the current tile ends.
 //   256x256x64 tiles through two 64 KiB LDS stages, so K-major rows are
