@@ -958,6 +958,64 @@ def _zipf_counts(E, M, seed, empty=(3, 17)):
     return c
 
 
+def _schedule_counts(E, tj, rounds, seed, blocks=256):
+    """Expert loads whose persistent fwd / dgrad schedule (tj n-tiles per m-tile)
+    holds about `rounds` rounds of `blocks` slots: a quarter of the experts thin (1-64
+    rows, their tiles two per slot), eight empty, the rest full m-tiles plus a partial
+    one of 65-256 rows."""
+    g = torch.Generator().manual_seed(seed)
+    nthin = E // 4
+    target = int((rounds - 0.5) * blocks)
+    mtiles = max((target - nthin * ((tj + 1) // 2)) // tj, E - nthin - 8)
+    counts = torch.zeros(E, dtype=torch.long)
+    counts[:nthin] = torch.randint(1, 65, (nthin,), generator=g)
+    rest = list(range(nthin + 8, E))
+    mt = torch.ones(len(rest), dtype=torch.long)
+    if mtiles > len(rest):
+        share = torch.multinomial(torch.ones(len(rest)), mtiles - len(rest), replacement=True,
+                                  generator=g)
+        mt += torch.bincount(share, minlength=len(rest))
+    for i, e in enumerate(rest):
+        counts[e] = (int(mt[i]) - 1) * 256 + int(torch.randint(65, 257, (1,), generator=g))
+    return counts[torch.randperm(E, generator=g)]
+
+
+@pytest.mark.parametrize("rounds,tj", [(1, 3), (7, 3), (12, 4), (14, 3), (6, 5)])
+def test_grouped_matmul_cost_sorted_schedule_exact(rounds, tj):
+    """Persistent fwd / dgrad launches of at most four n-tiles per m-tile and at most
+    twelve rounds of schedule slots take a cost-sorted slot assignment within each XCD,
+    computed by the kernel at start; longer launches and wider outputs keep the static
+    order. Both sides of each limit, into NaN-filled outputs with small-integer
+    operands: every row of every expert written, exactly. Thin experts (tiles two per
+    slot), partial m-tiles and full ones mixed."""
+    from torchturbo_amd import _lib
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    E, R = 96, 128
+    counts = _schedule_counts(E, tj, rounds, seed=rounds * 10 + tj)
+    M, J = int(counts.sum()), 256 * tj
+    g = torch.Generator(device=DEV).manual_seed(tj)
+    x = torch.randint(-2, 3, (M, R), generator=g, device=DEV).to(torch.bfloat16)
+    w1 = torch.randint(-2, 3, (E, R, J), generator=g, device=DEV).to(torch.bfloat16)
+    w2 = torch.randint(-2, 3, (E, J, R), generator=g, device=DEV).to(torch.bfloat16)
+    y = torch.full((M, J), float("nan"), dtype=torch.bfloat16, device=DEV)
+    dx = torch.full((M, J), float("nan"), dtype=torch.bfloat16, device=DEV)
+    cnt = counts.to(DEV)
+    bf = _lib.dtype_code(torch.bfloat16)
+    # fwd: y = x w1 (K = R, N = J); dgrad: dx = x w2^T (K = J, N = R): J-wide outputs
+    _lib.call("tt_gmm_fwd", _lib.ptr(x), _lib.ptr(w1), bf, M, R, J, E, 0, _lib.ptr(cnt),
+              _lib.ptr(y), _lib.stream())
+    _lib.call("tt_gmm_dgrad", _lib.ptr(x), _lib.ptr(w2), bf, M, J, R, E, 0, _lib.ptr(cnt),
+              _lib.ptr(dx), _lib.stream())
+    torch.cuda.synchronize()
+    s0 = 0
+    for e, c in enumerate(counts.tolist()):
+        xe = x[s0:s0 + c].float()
+        assert torch.equal(y[s0:s0 + c], (xe @ w1[e].float()).to(torch.bfloat16)), (e, c)
+        assert torch.equal(dx[s0:s0 + c], (xe @ w2[e].float().t()).to(torch.bfloat16)), (e, c)
+        s0 += c
+
+
 # Shapes of the Qwen3-30B-A3B layer's two GEMMs (fc1: K 2048 -> N 1536, fc2: K 768 ->
 # N 2048), tens of thousands of rows, Zipf loads with empty experts. Each launch has far
 @pytest.mark.parametrize("trans_b", [False, True])
